@@ -1,0 +1,121 @@
+"""ctypes binding of libaspec_amd.so, the HIP C ABI declared in include/aspec_amd.h.
+
+There is no fallback: if the library is missing or a call fails, an exception is raised.
+Status codes map to the reference's exception types (ValueError for layout violations,
+NotImplementedError for unsupported combinations, RuntimeError for HIP failures).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libaspec_amd.so"
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_size_p = ctypes.POINTER(ctypes.c_size_t)
+
+# name -> (restype, argtypes); the exact export list of include/aspec_amd.h.
+SIGNATURES = {
+    "aspec_abi_version": (_int, []),
+    "aspec_last_error": (ctypes.c_char_p, []),
+    "aspec_thd_row_metadata": (_int, [_c_void_p] * 5 + [_i64] * 6 + [_int] + [_c_void_p] * 5),
+    "aspec_thd_aux_endpoints": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _int,
+                                        _c_void_p, _c_void_p, _c_void_p]),
+    "aspec_thd_tile_metadata": (_int, [_c_void_p, _i64, _i64, _i64, _i64, _int] + [_c_void_p] * 10),
+    "aspec_dspark_plan_bytes": (_int, [_i64, _i64, _size_p]),
+    "aspec_dspark_plan_build": (_int, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
+    "aspec_dspark_attn_fwd": (
+        _int,
+        [_c_void_p, _i64, _i64] * 3
+        + [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32, _c_void_p, _i64, _i64,
+           _c_void_p, _c_void_p],
+    ),
+    "aspec_dspark_attn_bwd_workspace_bytes": (_int, [_i64, _i64, _size_p]),
+    "aspec_dspark_attn_bwd": (
+        _int,
+        [_c_void_p, _i64, _i64] * 5
+        + [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32]
+        + [_c_void_p, _i64, _i64] * 3
+        + [_c_void_p, _c_void_p],
+    ),
+    "aspec_dspark_attn_bwd_stages": (
+        _int,
+        [_int]
+        + [_c_void_p, _i64, _i64] * 5
+        + [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32]
+        + [_c_void_p, _i64, _i64] * 3
+        + [_c_void_p, _c_void_p],
+    ),
+    "aspec_loss_stats_floats": (_int, []),
+    "aspec_ce_l1_fwd": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64] + [_c_void_p] * 5
+    ),
+    "aspec_ce_l1_bwd": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64] + [_c_void_p] * 5
+    ),
+}
+
+ABI_VERSION = 1
+
+_lock = threading.Lock()
+_lib = None
+
+
+class AspecError(RuntimeError):
+    pass
+
+
+def load(path: Path | str | None = None) -> ctypes.CDLL:
+    """Load (once) and type the HIP library. Raises RuntimeError when it is absent."""
+    global _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        target = Path(path) if path is not None else LIBRARY_PATH
+        if not target.exists():
+            raise RuntimeError(
+                f"aspec_amd HIP library not built: {target} is missing "
+                "(run `python -m aspec_amd.build` or __graft_entry__.build())"
+            )
+        lib = ctypes.CDLL(str(target))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        if lib.aspec_abi_version() != ABI_VERSION:
+            raise RuntimeError("aspec_amd library ABI version mismatch; rebuild it")
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def check(status: int) -> None:
+    if status == 0:
+        return
+    message = (_lib.aspec_last_error() or b"").decode(errors="replace") if _lib else ""
+    if status == 1:
+        raise ValueError(message)
+    if status == 2:
+        raise NotImplementedError(message)
+    raise RuntimeError(message or f"aspec_amd call failed with status {status}")
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    check(getattr(lib, name)(*args))
+
+
+def ptr(tensor) -> int | None:
+    """Raw device pointer of a torch tensor (None for None)."""
+    return None if tensor is None else tensor.data_ptr()
+
+
+def stream_handle(device) -> int:
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

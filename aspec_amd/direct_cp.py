@@ -1,0 +1,377 @@
+"""Direct-CP / THD DSpark attention on MI355X (context-parallel degree 1).
+
+Mirrors the operator surface of aspec/models/ops/direct_cp.py: `DirectCPMetadata` (147-262),
+`direct_cp_attention_from_kv` (1047-1100), `direct_cp_attention` (1027-1044),
+`build_context_positions` (23-53) and `direct_cp_attention_observation` (265-284). Every GPU
+backend name the reference accepts ("auto", "fa4", "cudnn_flex_attention") and "hip" run the same
+HIP kernels; the reference's CPU "math" backend is not part of this product.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from aspec_amd import _lib, _timing
+
+MASK_VALUE = -1.0e30  # direct_cp.py:20
+
+_GPU_BACKENDS = {"auto", "hip", "fa4", "cudnn_flex_attention"}
+_GQA_MODES = {"auto", "native", "external", "internal"}
+
+
+def build_context_positions(total_positions: int, cp_rank: int, cp_size: int, *,
+                            layout: str = "contiguous", alignment: int = 1) -> Tensor:
+    """Positions owned by one CP rank (direct_cp.py:23-53). One GPU: CP=1 owns arange(total)."""
+    if total_positions < 0 or cp_size <= 0 or not 0 <= cp_rank < cp_size:
+        raise ValueError("invalid context-parallel position layout")
+    if layout not in {"contiguous", "zigzag"}:
+        raise ValueError(f"unsupported context-parallel layout: {layout}")
+    if cp_size != 1:
+        raise NotImplementedError("context parallelism > 1 needs several GPUs; this build is CP=1")
+    return torch.arange(total_positions, dtype=torch.long)
+
+
+class _ForwardSparseCache:
+    """Per-forward integer metadata shared by all layers (direct_cp.py:124-145): row metadata,
+    endpoints and the attention plan live here, never across forwards."""
+
+    def __init__(self):
+        self._entries = {}
+        self.thd_inputs = {}
+
+    def get(self, key):
+        return self._entries.get(key)
+
+    def __setitem__(self, key, value):
+        self._entries[key] = value
+
+    def values(self):
+        return self._entries.values()
+
+
+@dataclass
+class DirectCPMetadata:
+    """Replicated mask metadata plus this rank's context and query ownership (direct_cp.py:147-245)."""
+
+    anchor_positions: Tensor
+    block_keep_mask: Tensor
+    context_position_ids: Tensor
+    block_size: int
+    cp_rank: int
+    cp_size: int
+    group: Optional[object]
+    context_doc_ids: Optional[Tensor] = None
+    anchor_doc_ids: Optional[Tensor] = None
+    context_rope_position_ids: Optional[Tensor] = None
+    sequence_length: Optional[int] = None
+    backend: str = "fa4"
+    layout: str = "contiguous"
+    fa4_sparse: bool = True
+    context_window: Optional[int] = None
+    query_window: Optional[int] = None
+    draft_is_causal: bool = False
+    _fa4_cache: _ForwardSparseCache = field(default_factory=_ForwardSparseCache, repr=False)
+    attention_observation: dict = field(default_factory=dict, repr=False)
+
+    def __post_init__(self) -> None:
+        if self.anchor_positions.ndim != 2 or self.block_keep_mask.ndim != 2:
+            raise ValueError("anchor_positions and block_keep_mask must be [batch, blocks]")
+        if self.anchor_positions.shape != self.block_keep_mask.shape:
+            raise ValueError("anchor_positions and block_keep_mask shapes must match")
+        if self.context_position_ids.ndim != 2:
+            raise ValueError("context_position_ids must be [batch, local_context]")
+        if self.context_position_ids.shape[0] != self.anchor_positions.shape[0]:
+            raise ValueError("context and anchor batches must match")
+        if (self.context_doc_ids is None) != (self.anchor_doc_ids is None):
+            raise ValueError("context_doc_ids and anchor_doc_ids must be provided together")
+        if self.context_doc_ids is not None:
+            if self.context_doc_ids.shape != self.context_position_ids.shape:
+                raise ValueError("context_doc_ids must match context_position_ids")
+            if self.anchor_doc_ids.shape != self.anchor_positions.shape:
+                raise ValueError("anchor_doc_ids must match anchor_positions")
+        if (self.context_rope_position_ids is not None
+                and self.context_rope_position_ids.shape != self.context_position_ids.shape):
+            raise ValueError("context_rope_position_ids must match context_position_ids")
+        for name in ("context_window", "query_window"):
+            value = getattr(self, name)
+            if value is not None and (isinstance(value, bool) or not isinstance(value, int) or value <= 0):
+                raise ValueError(f"{name} must be a positive integer or null")
+        if not isinstance(self.draft_is_causal, bool):
+            raise ValueError("draft_is_causal must be boolean")
+        if self.block_size <= 0 or self.cp_size <= 0:
+            raise ValueError("block_size and cp_size must be positive")
+        if self.sequence_length is not None and self.sequence_length <= 0:
+            raise ValueError("sequence_length must be positive")
+        if not 0 <= self.cp_rank < self.cp_size:
+            raise ValueError("invalid CP rank")
+        if self.layout not in {"contiguous", "zigzag"}:
+            raise ValueError(f"unsupported context-parallel layout: {self.layout}")
+        divisor = 1 if self.cp_size == 1 else (self.cp_size if self.layout == "contiguous" else 2 * self.cp_size)
+        if self.num_blocks % divisor != 0:
+            raise ValueError(f"direct CP requires num_blocks divisible by {divisor} for {self.layout}")
+        if self.backend not in _GPU_BACKENDS | {"math"}:
+            raise ValueError(f"unsupported direct CP backend: {self.backend}")
+        if self.cp_size > 1 and self.group is None:
+            raise ValueError("a process group is required when cp_size > 1")
+
+    @property
+    def num_blocks(self) -> int:
+        return self.anchor_positions.shape[1]
+
+    @property
+    def blocks_per_rank(self) -> int:
+        return self.num_blocks // self.cp_size
+
+    @property
+    def queries_per_rank(self) -> int:
+        return self.blocks_per_rank * self.block_size
+
+    @property
+    def context_length(self) -> int:
+        return self.context_position_ids.shape[1]
+
+    @property
+    def local_block_ids(self) -> Tensor:
+        return torch.arange(self.num_blocks, dtype=torch.long)
+
+    @property
+    def collective_block_ids(self) -> Tensor:
+        return torch.arange(self.num_blocks, dtype=torch.long)
+
+
+def direct_cp_attention_observation(metadata: DirectCPMetadata) -> dict:
+    """Forward-scoped observation shared across metadata copies (direct_cp.py:265-284)."""
+    key = ("attention_observation", metadata.backend, metadata.context_window,
+           metadata.query_window, metadata.draft_is_causal)
+    observation = metadata._fa4_cache.get(key)
+    if observation is None:
+        observation = metadata.attention_observation
+        metadata._fa4_cache[key] = observation
+    return observation
+
+
+# ---------------------------------------------------------------------------------------------
+# Integer metadata (HIP): THD mask tensors, interval endpoints and the attention plan.
+# ---------------------------------------------------------------------------------------------
+class ThdRows:
+    """Device-resident row metadata of one forward: query_aux [4,Nq], key_aux [4,K] (int32),
+    endpoints [5,Nq] (int32) and the layout status flags."""
+
+    def __init__(self, query_aux, key_aux, endpoints, flags, num_queries, num_keys):
+        self.query_aux = query_aux
+        self.key_aux = key_aux
+        self.endpoints = endpoints
+        self.flags = flags
+        self.num_queries = num_queries
+        self.num_keys = num_keys
+        self._checked = False
+
+    def check_layout(self) -> None:
+        """Fail closed on layouts the interval form cannot represent (one host sync per forward,
+        as the reference's monotonic check at direct_cp.py:776-780)."""
+        if self._checked:
+            return
+        bad = int(self.flags.item())
+        if bad & 1:
+            raise ValueError("THD attention requires monotonically ordered context positions")
+        if bad & 2:
+            raise ValueError("THD attention requires contiguous ascending documents (padding last)")
+        self._checked = True
+
+
+def thd_row_metadata(metadata: DirectCPMetadata, device) -> ThdRows:
+    """HIP `aspec_thd_row_metadata`: `_query_metadata` / `_key_metadata`
+    (thd_attention.py:25-56) and `_build_cudnn_thd_mask` (direct_cp.py:750-900), cached per forward."""
+    device = torch.device(device)
+    key = ("hip_thd_rows", device)
+    rows = metadata._fa4_cache.thd_inputs.get(key)
+    if rows is not None:
+        return rows
+    if metadata.anchor_positions.shape[0] != 1:
+        raise ValueError("THD packing requires one controller-owned row per microbatch")
+    if metadata.cp_size != 1:
+        raise NotImplementedError("context parallelism > 1 needs several GPUs; this build is CP=1")
+    n, block, T = metadata.num_blocks, metadata.block_size, metadata.context_length
+    nq, nk = n * block, T + n * block
+    anchors = metadata.anchor_positions[0].to(device=device, dtype=torch.int64).contiguous()
+    keep = metadata.block_keep_mask[0].to(device=device, dtype=torch.bool).contiguous()
+    positions = metadata.context_position_ids[0].to(device=device, dtype=torch.int64).contiguous()
+    if metadata.context_doc_ids is None:
+        # Unpacked row: one document (the reference's packed=False mask at direct_cp.py:540-545).
+        anchor_docs = torch.zeros(n, dtype=torch.int64, device=device)
+        context_docs = torch.zeros(T, dtype=torch.int64, device=device)
+    else:
+        anchor_docs = metadata.anchor_doc_ids[0].to(device=device, dtype=torch.int64).contiguous()
+        context_docs = metadata.context_doc_ids[0].to(device=device, dtype=torch.int64).contiguous()
+    query_aux = torch.empty((4, nq), dtype=torch.int32, device=device)
+    key_aux = torch.empty((4, nk), dtype=torch.int32, device=device)
+    endpoints = torch.empty((5, nq), dtype=torch.int32, device=device)
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    seq = metadata.sequence_length if metadata.sequence_length is not None else 0
+    with _timing.region("thd_row_metadata"):
+        _lib.call(
+            "aspec_thd_row_metadata", _lib.ptr(anchors), _lib.ptr(keep), _lib.ptr(anchor_docs),
+            _lib.ptr(positions), _lib.ptr(context_docs), n, block, T, seq,
+            metadata.context_window or 0, metadata.query_window or 0, int(metadata.draft_is_causal),
+            _lib.ptr(query_aux), _lib.ptr(key_aux), _lib.ptr(endpoints), _lib.ptr(flags),
+            _lib.stream_handle(device),
+        )
+    rows = ThdRows(query_aux, key_aux, endpoints, flags, nq, nk)
+    metadata._fa4_cache.thd_inputs[key] = rows
+    return rows
+
+
+def attention_plan(metadata: DirectCPMetadata, rows: ThdRows, device) -> Tensor:
+    """HIP `aspec_dspark_plan_build`: the tile lists of the attention kernels, once per forward."""
+    key = ("hip_attention_plan", torch.device(device))
+    plan = metadata._fa4_cache.get(key)
+    if plan is not None:
+        return plan
+    import ctypes
+
+    size = ctypes.c_size_t()
+    _lib.call("aspec_dspark_plan_bytes", rows.num_queries, rows.num_keys, ctypes.byref(size))
+    plan = torch.empty(size.value, dtype=torch.uint8, device=device)
+    with _timing.region("attn_plan_build"):
+        _lib.call("aspec_dspark_plan_build", _lib.ptr(rows.endpoints), rows.num_queries,
+                  rows.num_keys, _lib.ptr(plan), _lib.stream_handle(device))
+    metadata._fa4_cache[key] = plan
+    return plan
+
+
+# ---------------------------------------------------------------------------------------------
+# Attention (HIP forward / backward behind autograd)
+# ---------------------------------------------------------------------------------------------
+def _thd_view(x: Tensor) -> Tensor:
+    """A [1, H, L, D] tensor whose rows the kernels can address: unit stride on D, 16-byte aligned
+    rows. Token-major ([1, L, H, D] storage) and head-major views both qualify as is."""
+    ok = (x.stride(3) == 1 and x.data_ptr() % 16 == 0
+          and x.stride(1) % 8 == 0 and x.stride(2) % 8 == 0)
+    return x if ok else x.transpose(1, 2).contiguous().transpose(1, 2)
+
+
+class _DSparkAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, query, key, value, endpoints, plan, scale):
+        q, k, v = _thd_view(query), _thd_view(key), _thd_view(value)
+        _, hq, nq, d = q.shape
+        hkv, nk = k.shape[1], k.shape[2]
+        out = torch.empty((1, nq, hq, v.shape[-1]), dtype=q.dtype, device=q.device)
+        lse = torch.empty((1, hq, nq), dtype=torch.float32, device=q.device)
+        with _timing.region("attn_fwd"):
+            _lib.call(
+                "aspec_dspark_attn_fwd",
+                _lib.ptr(q), q.stride(2), q.stride(1), _lib.ptr(k), k.stride(2), k.stride(1),
+                _lib.ptr(v), v.stride(2), v.stride(1), _lib.ptr(endpoints), _lib.ptr(plan),
+                nq, nk, hq, hkv, d, float(scale), _lib.ptr(out), out.stride(1), out.stride(2),
+                _lib.ptr(lse), _lib.stream_handle(q.device),
+            )
+        ctx.save_for_backward(q, k, v, out, lse, endpoints, plan)
+        ctx.scale = float(scale)
+        ctx.set_materialize_grads(False)
+        return out.transpose(1, 2), lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):
+        import ctypes
+
+        q, k, v, out, lse, endpoints, plan = ctx.saved_tensors
+        _, hq, nq, d = q.shape
+        hkv, nk = k.shape[1], k.shape[2]
+        if dout is None:
+            dout = torch.zeros((1, hq, nq, d), dtype=q.dtype, device=q.device)
+        dout = _thd_view(dout.to(q.dtype))
+        dlse_c = None if dlse is None else dlse.to(torch.float32).contiguous()
+        dq = torch.empty((1, nq, hq, d), dtype=q.dtype, device=q.device)
+        dk = torch.empty((1, nk, hkv, d), dtype=k.dtype, device=k.device)
+        dv = torch.empty((1, nk, hkv, v.shape[-1]), dtype=v.dtype, device=v.device)
+        size = ctypes.c_size_t()
+        _lib.call("aspec_dspark_attn_bwd_workspace_bytes", nq, hq, ctypes.byref(size))
+        workspace = torch.empty(size.value, dtype=torch.uint8, device=q.device)
+        outv = out.transpose(1, 2)
+        args = (
+            _lib.ptr(q), q.stride(2), q.stride(1), _lib.ptr(k), k.stride(2), k.stride(1),
+            _lib.ptr(v), v.stride(2), v.stride(1), _lib.ptr(out), outv.stride(2), outv.stride(1),
+            _lib.ptr(dout), dout.stride(2), dout.stride(1), _lib.ptr(lse), _lib.ptr(dlse_c),
+            _lib.ptr(endpoints), _lib.ptr(plan), nq, nk, hq, hkv, d, ctx.scale,
+            _lib.ptr(dq), dq.stride(1), dq.stride(2), _lib.ptr(dk), dk.stride(1), dk.stride(2),
+            _lib.ptr(dv), dv.stride(1), dv.stride(2), _lib.ptr(workspace),
+            _lib.stream_handle(q.device),
+        )
+        for stage, name in ((1, "attn_bwd_prepare"), (2, "attn_bwd_dq"), (4, "attn_bwd_dkdv")):
+            with _timing.region(name):
+                _lib.call("aspec_dspark_attn_bwd_stages", stage, *args)
+        return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None, None, None
+
+
+def dspark_attention(query: Tensor, key: Tensor, value: Tensor, metadata: DirectCPMetadata,
+                     scale: float) -> tuple[Tensor, Tensor]:
+    """HIP block-sparse DSpark attention over one packed THD row: (out [1,Hq,Nq,D], lse [1,Hq,Nq])."""
+    if not query.is_cuda:
+        raise ValueError("aspec_amd attention runs on the GPU; got a CPU tensor")
+    if query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
+        raise NotImplementedError("aspec_amd DSpark attention computes in bf16 (fp32 accumulation)")
+    if query.shape[0] != 1:
+        raise ValueError("THD packing requires one controller-owned row per microbatch")
+    if query.shape[1] % key.shape[1]:
+        raise ValueError("THD query heads must be divisible by KV heads")
+    if query.shape[2] != metadata.num_blocks * metadata.block_size:
+        raise ValueError("query rows must equal num_blocks * block_size")
+    rows = thd_row_metadata(metadata, query.device)
+    rows.check_layout()
+    plan = attention_plan(metadata, rows, query.device)
+    output, lse = _DSparkAttention.apply(query, key, value, rows.endpoints, plan, scale)
+    observation = direct_cp_attention_observation(metadata)
+    observation.update(
+        qkv_format="thd", kernel_backend="hip", kernel_mode="block_sparse_interval",
+        backward_strategy="hip_joint_gqa", gqa_layout="internal_joint", backward_observed=False,
+        context_parallel_size=metadata.cp_size, context_parallel_rank=metadata.cp_rank,
+        empty_local_partition=False, query_tokens=query.shape[2], key_tokens=key.shape[2],
+        context_tokens=metadata.context_length, context_window=metadata.context_window,
+        query_window=metadata.query_window, draft_is_causal=metadata.draft_is_causal,
+    )
+
+    def observe_backward(gradient):
+        observation["backward_observed"] = True
+        return gradient
+
+    for tensor in (output, lse):
+        if tensor.requires_grad:
+            tensor.register_hook(observe_backward)
+    return output, lse
+
+
+def direct_cp_attention_from_kv(query_own: Tensor, key: Tensor, value: Tensor,
+                                metadata: DirectCPMetadata, scale: Optional[float] = None, *,
+                                cudnn_gqa_mode: str = "auto") -> tuple[Tensor, Tensor]:
+    """Use already assembled context+draft KV (direct_cp.py:1047-1100)."""
+    length = metadata.context_length + metadata.queries_per_rank
+    if (key.ndim != 4 or value.ndim != 4 or key.shape[:3] != value.shape[:3]
+            or key.shape[0] != query_own.shape[0] or key.shape[2] != length):
+        raise ValueError("Combined KV must match local context and draft ownership")
+    scale = scale if scale is not None else query_own.shape[-1] ** -0.5
+    if cudnn_gqa_mode not in _GQA_MODES:
+        raise ValueError(f"unsupported cuDNN GQA mode: {cudnn_gqa_mode}")
+    if cudnn_gqa_mode != "auto" and metadata.backend != "cudnn_flex_attention":
+        raise ValueError("Explicit cudnn_gqa_mode requires the cuDNN backend")
+    if metadata.backend == "math":
+        raise NotImplementedError(
+            "the math backend is the reference's CPU path; aspec_amd runs the HIP kernels only")
+    if metadata.cp_size != 1:
+        raise NotImplementedError("context parallelism > 1 needs several GPUs; this build is CP=1")
+    output, lse = dspark_attention(query_own, key, value, metadata, scale)
+    return output.to(query_own.dtype), lse
+
+
+def direct_cp_attention(query_own: Tensor, context_key: Tensor, context_value: Tensor,
+                        draft_key_own: Tensor, draft_value_own: Tensor, metadata: DirectCPMetadata,
+                        scale: Optional[float] = None) -> tuple[Tensor, Tensor]:
+    """Concatenate context and draft KV, then attend (direct_cp.py:1027-1044)."""
+    return direct_cp_attention_from_kv(
+        query_own, torch.cat((context_key, draft_key_own), dim=2),
+        torch.cat((context_value, draft_value_own), dim=2), metadata, scale,
+    )

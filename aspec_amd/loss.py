@@ -1,0 +1,102 @@
+"""Selective-head loss kernels: cross-entropy and the fused CE + softmax-L1 (HIP).
+
+`cross_entropy` matches `F.cross_entropy(logits, targets, reduction="none")` as called at
+aspec/models/dspark.py:568-570 (ignore_index -100), computed in fp32 from bf16 logits.
+`ce_l1_from_logits` returns (ce, l1) per row from ONE read of the draft and teacher logits -- the
+two reductions share max / sum(exp) of the draft row -- and its backward writes dlogits once for
+both terms. It is what the DSpark head (`_prediction_terms`, dspark.py:553-636) needs per chunk.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from aspec_amd import _lib, _timing
+
+STATS = 8
+
+
+def _check_logits(logits):
+    if not logits.is_cuda:
+        raise ValueError("loss kernels require CUDA logits")
+    if logits.dtype != torch.bfloat16:
+        raise ValueError("loss kernels require BF16 logits")
+    if logits.ndim < 1 or logits.numel() == 0:
+        raise ValueError("loss kernels require nonempty logits with a vocabulary dimension")
+    if not logits.is_contiguous():
+        raise ValueError("loss kernels require contiguous logits")
+
+
+class _CeL1(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, logits, targets, teacher, indices, ignore_index):
+        vocab = logits.shape[-1]
+        rows = logits.numel() // vocab
+        dev = logits.device
+        stats = torch.empty((rows, STATS), dtype=torch.float32, device=dev)
+        ce = torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev)
+        l1 = torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev) if teacher is not None else None
+        flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        trows = teacher.shape[0] if (teacher is not None and indices is not None) else rows
+        with _timing.region("loss_fwd"):
+            _lib.call("aspec_ce_l1_fwd", _lib.ptr(logits), _lib.ptr(teacher), _lib.ptr(indices), trows,
+                      _lib.ptr(targets), ignore_index, rows, vocab, _lib.ptr(l1), _lib.ptr(ce),
+                      _lib.ptr(stats), _lib.ptr(flags), _lib.stream_handle(dev))
+        ctx.save_for_backward(logits, targets, teacher, indices, stats)
+        ctx.ignore_index = ignore_index
+        ctx.trows = trows
+        ctx.flags = flags
+        ctx.set_materialize_grads(False)
+        if l1 is None:
+            return ce, torch.zeros_like(ce)
+        return ce, l1
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, grad_ce, grad_l1):
+        logits, targets, teacher, indices, stats = ctx.saved_tensors
+        vocab = logits.shape[-1]
+        rows = logits.numel() // vocab
+        gce = None if grad_ce is None else grad_ce.to(torch.float32).contiguous()
+        gl1 = None if (grad_l1 is None or teacher is None) else grad_l1.to(torch.float32).contiguous()
+        grad_logits = torch.empty_like(logits)
+        if gce is None and gl1 is None:
+            return grad_logits.zero_(), None, None, None, None
+        with _timing.region("loss_bwd"):
+            _lib.call("aspec_ce_l1_bwd", _lib.ptr(logits), _lib.ptr(teacher), _lib.ptr(indices),
+                      ctx.trows, _lib.ptr(targets), ctx.ignore_index, rows, vocab, _lib.ptr(stats),
+                      _lib.ptr(gl1), _lib.ptr(gce), _lib.ptr(grad_logits),
+                      _lib.stream_handle(logits.device))
+        return grad_logits, None, None, None, None
+
+
+def ce_l1_from_logits(logits, targets, teacher=None, *, teacher_indices=None, ignore_index=-100):
+    """Per-row (cross-entropy, softmax-L1) from bf16 logits in one pass (HIP)."""
+    _check_logits(logits)
+    rows = logits.numel() // logits.shape[-1]
+    if targets.dtype != torch.int64 or targets.numel() != rows or targets.device != logits.device:
+        raise ValueError("targets must be one int64 class index per logit row on the logits device")
+    targets = targets.reshape(-1).contiguous()
+    if teacher is not None:
+        if teacher.requires_grad:
+            raise ValueError("tiled L1 requires frozen teacher logits")
+        if teacher.dtype != logits.dtype or not teacher.is_contiguous() or teacher.device != logits.device:
+            raise ValueError("draft and teacher logits must share shape and dtype")
+        if teacher_indices is None and teacher.shape != logits.shape:
+            raise ValueError("draft and teacher logits must share shape and dtype")
+        if teacher_indices is not None and (
+                teacher.ndim != 2 or teacher.shape[-1] != logits.shape[-1] or teacher.shape[0] == 0
+                or teacher_indices.dtype != torch.int64 or teacher_indices.numel() != rows
+                or teacher_indices.device != logits.device):
+            raise ValueError("indexed teacher requires a nonempty 2D table and one contiguous CUDA "
+                             "int64 index per Draft row")
+        if teacher_indices is not None:
+            teacher_indices = teacher_indices.reshape(-1).contiguous()
+    return _CeL1.apply(logits, targets, teacher, teacher_indices, ignore_index)
+
+
+def cross_entropy(logits, targets, ignore_index=-100):
+    """Per-row cross-entropy of bf16 logits [..., V] against int64 targets (fp32 result)."""
+    ce, _ = ce_l1_from_logits(logits, targets, None, ignore_index=ignore_index)
+    return ce

@@ -1,0 +1,313 @@
+"""DSpark draft hot-path benchmark on one MI355X (Qwen3-8B geometry, 4K packed).
+
+One step = one packed 4096-token row through the draft hot path, inputs resident in HBM:
+  1. THD row metadata + attention plan (HIP integer kernels),
+  2. DSpark block-sparse attention forward (HIP, bf16 MFMA, GQA 32/8 x 128, 512 anchors x 16),
+  3. selective-head projection: draft logits = O[8192, 4096] @ W^T (W [32000, 4096], hipBLASLt) and
+     the frozen-teacher table = target_hidden[4096, 4096] @ W^T (no grad),
+  4. fused CE + softmax-L1 (HIP, indexed teacher rows), objective (0.1 CE + 0.9 L1) weighted by the
+     DSpark eval mask x exp(-k/4) decay, normalised by the weight sum,
+  5. backward: dlogits (HIP), dO = dlogits @ W (hipBLASLt), attention backward (HIP).
+Metric: input context tokens per second (4096 per step / wall time), as the reference's draft-only
+benchmark defines it (tools/performance/torchspec_benchmark.py:688,764).
+
+Prints ONE JSON line. `--gpus N` with N > 1 exits: this build runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "draft-only input tokens/s (1 GPU, Qwen3-8B 4K packed); attn fwd+bwd % MFMA peak"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+VOCAB = 32000
+HIDDEN = 4096
+DECAY_GAMMA = 4.0
+CE_ALPHA, L1_ALPHA = 0.1, 0.9
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-cpu-baseline", action="store_true", help="skip the timed CPU oracle leg")
+    p.add_argument("--no-kernel-timing", action="store_true", help="no per-kernel HIP events")
+    return p.parse_args()
+
+
+def build_inputs(device, seed):
+    import torch
+
+    from aspec_amd import workloads as W
+
+    w = W.config2()
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    nq, nk = w.num_queries, w.num_keys
+
+    def randn(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(device=device, dtype=torch.bfloat16)
+
+    x = {
+        "w": w,
+        # token-major storage, [1, H, L, D] views (what DFlashAttention hands the op)
+        "q": randn(1, nq, w.q_heads, w.head_dim, scale=0.5).transpose(1, 2).requires_grad_(),
+        "k": randn(1, nk, w.kv_heads, w.head_dim, scale=0.5).transpose(1, 2).requires_grad_(),
+        "v": randn(1, nk, w.kv_heads, w.head_dim, scale=0.5).transpose(1, 2).requires_grad_(),
+        "head": randn(VOCAB, HIDDEN, scale=0.02),
+        "target_hidden": randn(w.context_length, HIDDEN),
+    }
+    ids = torch.randint(0, VOCAB, (w.context_length,), generator=g)
+    anchors = torch.as_tensor(w.anchors)
+    B = w.block_size
+    label = anchors[:, None] + torch.arange(1, B + 1)[None]            # dspark.py:240-246
+    valid = label < w.sequence_length
+    safe = label.clamp(max=w.sequence_length - 1)
+    eval_mask = (valid & torch.as_tensor(w.keep)[:, None]).int().cumprod(-1).float()
+    decay = torch.exp(-torch.arange(B).float() / DECAY_GAMMA)           # dspark.py:163-172
+    x["targets"] = ids[safe].reshape(-1).to(device)
+    x["weights"] = (eval_mask * decay).reshape(-1).to(device)
+    x["teacher_index"] = (safe - 1).clamp(min=0).reshape(-1).to(device)  # dspark.py:381-383
+    t = lambda a, dt: torch.as_tensor(a, dtype=dt, device=device)[None]  # noqa: E731
+    x["meta_tensors"] = (t(w.anchors, torch.long), t(w.keep, torch.bool), t(w.context_positions, torch.long),
+                         t(w.ctx_doc_ids, torch.long), t(w.anchor_doc_ids, torch.long))
+    return x
+
+
+class _Head:
+    """Selective-head projection with HIP-event regions around both GEMMs."""
+
+    @staticmethod
+    def make():
+        import torch
+
+        from aspec_amd import _timing
+
+        class HeadProjection(torch.autograd.Function):
+            @staticmethod
+            def forward(ctx, hidden, weight):
+                with _timing.region("head_gemm_fwd"):
+                    out = torch.matmul(hidden, weight.t())
+                ctx.save_for_backward(weight)
+                return out
+
+            @staticmethod
+            def backward(ctx, grad):
+                (weight,) = ctx.saved_tensors
+                with _timing.region("head_gemm_dgrad"):
+                    dh = torch.matmul(grad, weight)
+                return dh, None
+
+        return HeadProjection
+
+
+def step(x, head_fn):
+    import torch
+
+    from aspec_amd import _timing
+    from aspec_amd.direct_cp import DirectCPMetadata, direct_cp_attention_from_kv
+    from aspec_amd.loss import ce_l1_from_logits
+
+    w = x["w"]
+    anchors, keep, pos, docs, adocs = x["meta_tensors"]
+    meta = DirectCPMetadata(anchors, keep, pos, w.block_size, 0, 1, None, context_doc_ids=docs,
+                            anchor_doc_ids=adocs, sequence_length=w.sequence_length)
+    for name in ("q", "k", "v"):
+        x[name].grad = None
+    out, _ = direct_cp_attention_from_kv(x["q"], x["k"], x["v"], meta)
+    hidden = out.transpose(1, 2).reshape(w.num_queries, w.q_heads * w.head_dim)
+    logits = head_fn.apply(hidden, x["head"])
+    with torch.no_grad(), _timing.region("teacher_gemm"):
+        teacher = torch.matmul(x["target_hidden"], x["head"].t())
+    ce, l1 = ce_l1_from_logits(logits, x["targets"], teacher, teacher_indices=x["teacher_index"])
+    wts = x["weights"]
+    loss = (CE_ALPHA * (ce * wts).sum() + L1_ALPHA * (l1 * wts).sum()) / wts.sum().clamp(min=1e-6)
+    loss.backward()
+    return loss
+
+
+def kernel_work(w):
+    """Algorithmic work per launch of each timed region (FLOPs for MFMA-bound, bytes for HBM-bound)."""
+    from oracle import metadata as M
+
+    ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
+                       w.block_size, w.sequence_length)
+    pairs = M.visible_pairs(ends)
+    hd = w.q_heads * w.head_dim
+    rows, ctx = w.num_queries, w.context_length
+    return pairs, {
+        "attn_fwd": ("mfma", 4 * hd * pairs),
+        "attn_bwd_dq": ("mfma", 6 * hd * pairs),       # S, dP recompute + dS.K
+        "attn_bwd_dkdv": ("mfma", 8 * hd * pairs),     # S, dP recompute + P^T.dO + dS^T.Q
+        "attn_bwd_prepare": ("hbm", rows * w.q_heads * (2 * w.head_dim * 2 + 4 * 3)),
+        "head_gemm_fwd": ("mfma", 2 * rows * VOCAB * HIDDEN),
+        "head_gemm_dgrad": ("mfma", 2 * rows * VOCAB * HIDDEN),
+        "teacher_gemm": ("mfma", 2 * ctx * VOCAB * HIDDEN),
+        "loss_fwd": ("hbm", 2 * rows * VOCAB * 2),
+        "loss_bwd": ("hbm", 3 * rows * VOCAB * 2),
+        "thd_row_metadata": ("hbm", w.num_blocks * 17 + ctx * 16 + rows * 4 * 4 + w.num_keys * 4 * 4 + rows * 5 * 4),
+        "attn_plan_build": ("hbm", rows * 5 * 4 * 2),
+    }
+
+
+def cpu_baseline(x, seed):
+    """The oracle (the reference's math path restated, fp32, autograd) timed on host cores on a
+    bounded sample of the same step, extrapolated linearly to one full step."""
+    import torch
+
+    from oracle import attention as A
+    from oracle import loss as L  # noqa: F401  (loss oracle is numpy fp64; CPU baseline uses torch fp32)
+    from oracle import metadata as M
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    w = x["w"]
+    g = torch.Generator().manual_seed(seed)
+    group = w.q_heads // w.kv_heads
+    ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
+                       w.block_size, w.sequence_length)
+    t0 = time.perf_counter()
+    vis = M.endpoints_to_dense(ends, w.num_keys)
+    t_meta = time.perf_counter() - t0
+    # attention: one KV group (1 of Hkv) fwd+bwd in fp32 with autograd
+    q = torch.randn(group, w.num_queries, w.head_dim, generator=g) * 0.5
+    k = torch.randn(1, w.num_keys, w.head_dim, generator=g) * 0.5
+    v = torch.randn(1, w.num_keys, w.head_dim, generator=g) * 0.5
+    dout = torch.randn(group, w.num_queries, w.head_dim, generator=g)
+    t0 = time.perf_counter()
+    A.attention(q, k, v, vis, w.head_dim ** -0.5, dout=dout, dtype=torch.float32)
+    t_attn = time.perf_counter() - t0
+    del q, k, v, dout
+    # head + CE + L1 on a row sample (fp32, autograd)
+    rows_s, ctx_s = 256, 128
+    hidden = (torch.randn(rows_s, HIDDEN, generator=g)).requires_grad_()
+    weight = torch.randn(VOCAB, HIDDEN, generator=g) * 0.02
+    th = torch.randn(ctx_s, HIDDEN, generator=g)
+    tgt = torch.randint(0, VOCAB, (rows_s,), generator=g)
+    tidx = torch.randint(0, ctx_s, (rows_s,), generator=g)
+    t0 = time.perf_counter()
+    logits = hidden @ weight.t()
+    with torch.no_grad():
+        teacher = (th @ weight.t())[tidx]
+    ce = torch.nn.functional.cross_entropy(logits, tgt, reduction="none")
+    l1 = (torch.softmax(logits, -1) - torch.softmax(teacher, -1)).abs().sum(-1)
+    (CE_ALPHA * ce.sum() + L1_ALPHA * l1.sum()).backward()
+    t_head = time.perf_counter() - t0
+    est = t_meta + t_attn * w.kv_heads + t_head * (w.num_queries / rows_s)
+    return {
+        "value": round(w.context_length / est, 3),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle fp32 (torch CPU, autograd): attention fwd+bwd for 1 of {w.kv_heads} KV groups "
+                   f"({group} q heads x {w.num_queries} queries x {w.num_keys} keys, dense masked math path) "
+                   f"took {t_attn:.2f} s (x{w.kv_heads}); head GEMM + CE + L1 fwd/bwd on {rows_s} of "
+                   f"{w.num_queries} rows took {t_head:.2f} s (x{w.num_queries // rows_s}); dense mask "
+                   f"{t_meta:.2f} s; extrapolated step {est:.1f} s"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus_requested": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    from aspec_amd import _lib, _timing
+
+    _lib.load()  # fail loudly if the HIP library is missing
+    device = torch.device("cuda:0")
+    x = build_inputs(device, args.seed)
+    head_fn = _Head.make()
+    w = x["w"]
+
+    for _ in range(args.warmup):
+        step(x, head_fn)
+    torch.cuda.synchronize()
+    _timing.reset()
+    _timing.enable(not args.no_kernel_timing)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step(x, head_fn)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    _timing.enable(False)
+    kernels = _timing.summary() if not args.no_kernel_timing else {}
+    if not torch.isfinite(loss):
+        raise RuntimeError("non-finite loss in the timed steps")
+
+    pairs, work = kernel_work(w)
+    per_kernel = {}
+    for name, stats in kernels.items():
+        bound, amount = work.get(name, (None, None))
+        entry = {"mean_ms": round(stats["mean_ms"], 4), "launches": stats["launches"]}
+        if bound == "mfma":
+            tf = amount / (stats["mean_ms"] * 1e-3) / 1e12
+            entry.update(tflops=round(tf, 2), frac_mfma=round(tf / PEAK_BF16_TFLOPS, 4))
+        elif bound == "hbm":
+            gbs = amount / (stats["mean_ms"] * 1e-3) / 1e9
+            entry.update(gbs=round(gbs, 1), frac_hbm=round(gbs / PEAK_HBM_GBS, 4))
+        per_kernel[name] = entry
+    roofline = None
+    if kernels:
+        dominant = max(kernels, key=lambda n: kernels[n]["total_ms"])
+        bound, amount = work[dominant]
+        ms = kernels[dominant]["mean_ms"]
+        if bound == "mfma":
+            ach, peak, unit = amount / (ms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s"
+        else:
+            ach, peak, unit = amount / (ms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+        roofline = {"kernel": dominant, "bound": bound, "achieved": round(ach, 2), "peak": peak,
+                    "unit": unit, "frac": round(ach / peak, 4), "traffic": None,
+                    "algorithmic_per_launch": amount}
+    attn = None
+    if all(k in kernels for k in ("attn_fwd", "attn_bwd_prepare", "attn_bwd_dq", "attn_bwd_dkdv")):
+        t_fb = sum(kernels[k]["mean_ms"] for k in ("attn_fwd", "attn_bwd_prepare", "attn_bwd_dq", "attn_bwd_dkdv"))
+        flops = 14 * w.q_heads * w.head_dim * pairs  # reference accounting: fwd 4 + bwd 10
+        attn = {"fwd_bwd_ms": round(t_fb, 4), "tflops": round(flops / (t_fb * 1e-3) / 1e12, 2),
+                "frac_mfma": round(flops / (t_fb * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                "visible_pairs_per_head": pairs, "gflop_fwd_bwd": round(flops / 1e9, 1)}
+
+    result = {
+        "metric": METRIC,
+        "value": round(w.context_length * args.steps / elapsed, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) inputs, random-init head, random token ids)",
+        "config": {
+            "workload": "config2: Qwen3-8B geometry, one 4096-token document, 512 anchors x block 16 "
+                        "(8192 draft queries, 12288 keys), GQA 32/8 x 128, selective head V=32000 "
+                        "(CE + tiled L1, indexed teacher)",
+            "context_tokens": w.context_length, "draft_queries": w.num_queries,
+            "parallelism": "single GPU, CP=1",
+        },
+        "roofline": roofline,
+        "attention": attn,
+        "kernels": per_kernel,
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(x, args.seed)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

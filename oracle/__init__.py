@@ -1,0 +1,18 @@
+"""CPU oracle for the DSpark draft hot path -- TEST INFRASTRUCTURE ONLY.
+
+A restatement, in numpy (integer metadata) and CPU torch / numpy fp64 (attention and loss
+arithmetic), of the reference's algorithms on this path, each function citing the reference
+file:line it follows. Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of
+`bench.py` may import this package, and only as the checker or the timed CPU baseline; the
+`aspec_amd` product never imports it and never falls back to it.
+
+How each part is pinned (besides agreeing with the HIP path):
+  metadata.py  -- three independent restatements (mask_mod brute force, math `_visibility`,
+                  searchsorted endpoints) must agree; hand-derived golden fixtures
+                  (tests/golden/thd_small_case.json, dflash_truth_tables.json) from the reference's
+                  own test cases; tile classes equal brute-force any/all (the reference's spec).
+  attention.py -- reduces to textbook masked softmax attention; pinned by a per-row float64 loop,
+                  single-visible-key closed forms and autograd-vs-finite-difference gradients.
+  loss.py      -- fp64 closed forms pinned by special values (identical rows -> 0, disjoint
+                  one-hots -> 2, uniform CE -> log V) and finite-difference gradients.
+"""

@@ -1,0 +1,157 @@
+"""HIP DSpark attention forward/backward vs the fp32 math oracle.
+
+Tolerances (bf16 inputs, fp32 accumulation) follow the reference's own bf16-GPU-vs-math bars
+(tests/test_thd_attention.py:218-225): atol = rtol = 0.025 for O and LSE, 0.04 for dQ/dK/dV.
+Max-abs and relative-L2 errors are printed for every case.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from aspec_amd import workloads as W
+from aspec_amd.direct_cp import direct_cp_attention_from_kv
+from oracle import attention as A
+from oracle import metadata as M
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(w, device, seed, scale_in=0.5, token_major=True):
+    g = torch.Generator().manual_seed(seed)
+    hq, hkv, d = w.q_heads, w.kv_heads, w.head_dim
+    q = (torch.randn(w.num_queries, hq, d, generator=g) * scale_in).bfloat16()
+    k = (torch.randn(w.num_keys, hkv, d, generator=g) * scale_in).bfloat16()
+    v = (torch.randn(w.num_keys, hkv, d, generator=g) * scale_in).bfloat16()
+    dout = torch.randn(w.num_queries, hq, d, generator=g).bfloat16()
+    dlse = torch.randn(hq, w.num_queries, generator=g) * 0.1
+    def dev(x):
+        x = x.to(device)[None].transpose(1, 2)  # [1, H, L, D] view of token-major storage
+        return x if token_major else x.contiguous()
+    return [dev(x).requires_grad_() for x in (q, k, v)], dev(dout), dlse.to(device)[None]
+
+
+def _report(name, got, ref):
+    got, ref = got.double().cpu(), ref.double().cpu()
+    err = (got - ref).abs().max().item()
+    rel = ((got - ref).norm() / ref.norm().clamp_min(1e-30)).item()
+    print(f"{name}: max_abs={err:.3e} rel_l2={rel:.3e}")
+    return err, rel
+
+
+def _check(w, device, seed=0, masks=None, token_major=True, use_dlse=True):
+    masks = masks or {}
+    (q, k, v), dout, dlse = _inputs(w, device, seed, token_major=token_major)
+    meta = W.metadata_for(w, device, **masks)
+    scale = w.head_dim ** -0.5
+    out, lse = direct_cp_attention_from_kv(q, k, v, meta, scale)
+    obj = (out.float() * dout.float()).sum()
+    if use_dlse:
+        obj = obj + (lse * dlse).sum()
+    obj.backward()
+    torch.cuda.synchronize()
+
+    ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
+                       w.block_size, w.sequence_length, **masks)
+    vis = M.endpoints_to_dense(ends, w.num_keys)
+    cpu = lambda x: x.detach()[0].float().cpu()  # noqa: E731
+    r_out, r_lse, (r_dq, r_dk, r_dv) = A.attention(
+        cpu(q), cpu(k), cpu(v), vis, scale, dout=cpu(dout),
+        dlse=cpu(dlse) if use_dlse else None, dtype=torch.float32)
+    keep = torch.as_tensor(vis.any(-1))
+    _report("O", cpu(out), r_out)
+    torch.testing.assert_close(cpu(out), r_out, atol=0.025, rtol=0.025)
+    assert torch.all(cpu(lse)[:, ~keep] == A.MASK_VALUE)
+    assert torch.all(cpu(out)[:, ~keep] == 0)
+    _report("LSE", cpu(lse)[:, keep], r_lse[:, keep])
+    torch.testing.assert_close(cpu(lse)[:, keep], r_lse[:, keep], atol=0.025, rtol=0.025)
+    for name, got, ref in (("dQ", q.grad, r_dq), ("dK", k.grad, r_dk), ("dV", v.grad, r_dv)):
+        _report(name, cpu(got), ref)
+        torch.testing.assert_close(cpu(got), ref, atol=0.04, rtol=0.04)
+    return meta
+
+
+def test_reference_large_gpu_layout(gpu):
+    """The reference's _large_gpu_check layout (tests/test_thd_attention.py:175-226): documents
+    257/263/19, anchors linspace(0, 537, 80), block 7, block 13 dropped, GQA 4/2 x 128."""
+    lengths = [257, 263, 19]
+    docs = np.concatenate([np.full(n, i) for i, n in enumerate(lengths)])
+    anchors = np.linspace(0, 537, 80).astype(np.int64)
+    keep = np.ones(80, bool)
+    keep[13] = False
+    w = W.from_layout("ref_large", lengths, anchors, docs[anchors], 7, keep=keep, q_heads=4, kv_heads=2)
+    meta = _check(w, gpu, seed=79)
+    assert meta.attention_observation["backward_observed"]
+    assert meta.attention_observation["qkv_format"] == "thd"
+
+
+@pytest.mark.parametrize("block", [1, 7, 31])
+def test_reference_metadata_layouts(gpu, block):
+    w = W.reference_test_layout(block)
+    w.q_heads, w.kv_heads = 8, 2
+    _check(w, gpu, seed=block)
+
+
+@pytest.mark.parametrize("masks", [{"query_window": 5, "draft_is_causal": True}, {"context_window": 40}],
+                         ids=str)
+def test_windows_and_causal(gpu, masks):
+    w = W.reference_test_layout(7, drop_doc=False)
+    w.q_heads, w.kv_heads = 8, 2
+    _check(w, gpu, seed=11, masks=masks)
+
+
+def test_config1_fwd_bwd(gpu):
+    _check(W.config1(0), gpu, seed=0)
+
+
+def test_config1_head_major_inputs_without_dlse(gpu):
+    _check(W.config1(1), gpu, seed=1, token_major=False, use_dlse=False)
+
+
+def test_gqa_group_of_five(gpu):
+    w = W.config1(2)
+    w.q_heads, w.kv_heads = 10, 2
+    _check(w, gpu, seed=2)
+
+
+def test_no_active_queries_gives_zero_outputs_and_gradients(gpu):
+    w = W.config1(0)
+    w.keep = np.zeros_like(w.keep)
+    (q, k, v), dout, _ = _inputs(w, gpu, 0)
+    meta = W.metadata_for(w, gpu)
+    out, lse = direct_cp_attention_from_kv(q, k, v, meta)
+    out.float().sum().backward()
+    assert not out.any() and torch.all(lse == A.MASK_VALUE)
+    assert not q.grad.any() and not k.grad.any() and not v.grad.any()
+
+
+def test_config2_full_size_properties(gpu):
+    """Config 2 at full size: sampled rows against the float64 row loop, plus size-independent
+    identities of the backward: sum_k dV[k] = sum over the GQA group of sum_q dO[q] (rows of P sum
+    to 1) and sum_k dK[k] = 0 (rows of dS sum to 0 when dLSE = 0)."""
+    w = W.config2()
+    (q, k, v), dout, _ = _inputs(w, gpu, 5)
+    meta = W.metadata_for(w, gpu)
+    out, lse = direct_cp_attention_from_kv(q, k, v, meta)
+    (out.float() * dout.float()).sum().backward()
+    torch.cuda.synchronize()
+    ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
+                       w.block_size, w.sequence_length)
+    rng = np.random.default_rng(0)
+    rows = rng.choice(w.num_queries, 12, replace=False)
+    qc, kc, vc = (x.detach()[0].float().cpu() for x in (q, k, v))
+    vis_rows = M.endpoints_to_dense(ends[:, rows], w.num_keys)
+    for head in (0, 13, 31):
+        for i, r in enumerate(rows):
+            vis = np.zeros((w.num_queries, w.num_keys), bool) if i == 0 else vis
+            vis[r] = vis_rows[i]
+            o_ref, l_ref = A.attention_row_loop(qc, kc, vc, vis, w.head_dim ** -0.5, head, r)
+            np.testing.assert_allclose(out[0, head, r].float().cpu().numpy(), o_ref, atol=0.025, rtol=0.025)
+            assert abs(float(lse[0, head, r]) - l_ref) < 0.025
+    group = w.q_heads // w.kv_heads
+    dsum = dout.detach()[0].float().sum(1).view(w.kv_heads, group, -1).sum(1)
+    _report("sum dV vs sum dO", v.grad[0].float().sum(1), dsum)
+    torch.testing.assert_close(v.grad[0].float().sum(1), dsum, atol=0.5, rtol=0.02)
+    dk_sum = k.grad[0].float().sum(1)
+    scale_ref = k.grad[0].float().abs().sum(1)
+    assert torch.all(dk_sum.abs() <= 0.02 * scale_ref + 0.05)
