@@ -41,7 +41,21 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the timed CPU oracle leg")
     p.add_argument("--no-kernel-timing", action="store_true", help="no per-kernel HIP events")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run a plain device copy of MIB MiB (5 times): the reference kernel that "
+                        "scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
     return p.parse_args()
+
+
+def copy_calibration(mib: int) -> None:
+    import torch
+
+    src = torch.ones(mib * 2**20 // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_mib": mib, "bytes_read": mib * 2**20, "bytes_written": mib * 2**20}))
 
 
 def build_inputs(device, seed):
@@ -158,6 +172,26 @@ def kernel_work(w):
     }
 
 
+_REGION_KERNEL = {"attn_fwd": "attn_fwd_kernel", "attn_bwd_dq": "attn_bwd_dq_kernel",
+                  "attn_bwd_dkdv": "attn_bwd_dkdv_kernel", "attn_bwd_prepare": "attn_bwd_pre_kernel",
+                  "loss_fwd": "void loss_fwd_resident<4>", "loss_bwd": "void loss_bwd_kernel<true>"}
+
+
+def measured_traffic(region):
+    """HBM bytes per launch (read + write) of a region's kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
+    from pathlib import Path
+
+    path = Path(__file__).resolve().parent / "profiles" / "dspark_config2_hbm_traffic.json"
+    kernel = _REGION_KERNEL.get(region)
+    if kernel is None or not path.exists():
+        return None
+    entry = json.loads(path.read_text())["kernels"].get(kernel)
+    if entry is None:
+        return None
+    return int(entry["read_bytes"] + entry["write_bytes"])
+
+
 def cpu_baseline(x, seed):
     """The oracle (the reference's math path restated, fp32, autograd) timed on host cores on a
     bounded sample of the same step, extrapolated linearly to one full step."""
@@ -221,6 +255,9 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
                           "n_gpus_requested": args.gpus}))
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     import torch
 
     from aspec_amd import _lib, _timing
@@ -269,7 +306,7 @@ def main():
         else:
             ach, peak, unit = amount / (ms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
         roofline = {"kernel": dominant, "bound": bound, "achieved": round(ach, 2), "peak": peak,
-                    "unit": unit, "frac": round(ach / peak, 4), "traffic": None,
+                    "unit": unit, "frac": round(ach / peak, 4), "traffic": measured_traffic(dominant),
                     "algorithmic_per_launch": amount}
     attn = None
     if all(k in kernels for k in ("attn_fwd", "attn_bwd_prepare", "attn_bwd_dq", "attn_bwd_dkdv")):

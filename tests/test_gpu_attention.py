@@ -146,8 +146,8 @@ def test_config2_full_size_properties(gpu):
             vis = np.zeros((w.num_queries, w.num_keys), bool) if i == 0 else vis
             vis[r] = vis_rows[i]
             o_ref, l_ref = A.attention_row_loop(qc, kc, vc, vis, w.head_dim ** -0.5, head, r)
-            np.testing.assert_allclose(out[0, head, r].float().cpu().numpy(), o_ref, atol=0.025, rtol=0.025)
-            assert abs(float(lse[0, head, r]) - l_ref) < 0.025
+            np.testing.assert_allclose(out[0, head, r].detach().float().cpu().numpy(), o_ref, atol=0.025, rtol=0.025)
+            assert abs(float(lse[0, head, r].detach()) - l_ref) < 0.025
     group = w.q_heads // w.kv_heads
     dsum = dout.detach()[0].float().sum(1).view(w.kv_heads, group, -1).sum(1)
     _report("sum dV vs sum dO", v.grad[0].float().sum(1), dsum)

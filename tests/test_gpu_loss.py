@@ -26,7 +26,7 @@ def test_tiled_l1_matches_fp64_oracle_and_bf16_gradient(gpu, vocab, scale):
     xd, yd = draft.double().cpu().numpy(), target.double().cpu().numpy()
     ref = L.l1(xd, yd)
     ref_grad = torch.as_tensor(L.l1_grad(xd, yd, upstream.double().cpu().numpy()))
-    np.testing.assert_allclose(loss.double().cpu().numpy(), ref, atol=2e-6, rtol=2e-6)
+    np.testing.assert_allclose(loss.detach().double().cpu().numpy(), ref, atol=2e-6, rtol=2e-6)
     rel = ((grad.double().cpu() - ref_grad).norm() / ref_grad.norm()).item()
     print(f"L1 V={vocab} scale={scale}: grad rel_l2={rel:.2e}")
     assert rel < 0.01
@@ -128,8 +128,8 @@ def test_cross_entropy_and_fused_gradient(gpu, vocab):
     ce, l1 = ce_l1_from_logits(xin, t, y)
     ((ce * gce).sum() + (l1 * gl1).sum()).backward()
     xd, yd, td = x.double().cpu().numpy(), y.double().cpu().numpy(), t.cpu().numpy()
-    np.testing.assert_allclose(ce.double().cpu().numpy(), L.cross_entropy(xd, td), atol=2e-5, rtol=2e-6)
-    np.testing.assert_allclose(l1.double().cpu().numpy(), L.l1(xd, yd), atol=2e-6, rtol=2e-6)
+    np.testing.assert_allclose(ce.detach().double().cpu().numpy(), L.cross_entropy(xd, td), atol=2e-5, rtol=2e-6)
+    np.testing.assert_allclose(l1.detach().double().cpu().numpy(), L.l1(xd, yd), atol=2e-6, rtol=2e-6)
     ref = torch.as_tensor(L.cross_entropy_grad(xd, td, gce.double().cpu().numpy())
                           + L.l1_grad(xd, yd, gl1.double().cpu().numpy()))
     rel = ((xin.grad.double().cpu() - ref).norm() / ref.norm()).item()
