@@ -35,7 +35,7 @@ SIGNATURES = {
         + [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32, _c_void_p, _i64, _i64,
            _c_void_p, _c_void_p],
     ),
-    "aspec_dspark_attn_bwd_workspace_bytes": (_int, [_i64, _i64, _size_p]),
+    "aspec_dspark_attn_bwd_workspace_bytes": (_int, [_i64, _i64, _i64, _i64, _size_p]),
     "aspec_dspark_attn_bwd": (
         _int,
         [_c_void_p, _i64, _i64] * 5
@@ -60,7 +60,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib = None

@@ -98,11 +98,61 @@ __device__ __forceinline__ void stage_tile(const uint16_t* __restrict__ src, int
   }
 }
 
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+
+__device__ __forceinline__ s16x4 ds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(__attribute__((address_space(3))) void*)p);
+}
+
+// A operand whose rows are the columns of a row-major LDS tile (a transposed fragment), read with
+// gfx950's transpose load ds_read_b64_tr_b16. Within each 16-lane group, lane i receives element
+// i%4 of the 8-byte chunks that lanes i/4, i/4+4, i/4+8 and i/4+12 of its group address. Lane s
+// therefore addresses row rsub(s) = (s/32)*4 + (s%16)/4 and columns csub(s) = 16*((s/16)%2) +
+// 4*(s%4) .. +3, and lane L = 32g + i ends up holding column col0 + i of rows
+// row0 + {g*4 + e} (e < 4, first read) and row0 + {8 + g*4 + e-4} (second read): exactly the
+// (g, e) reduction slots read_split_operand() / pack_c_half() use.
+__device__ __forceinline__ bf16x8 read_tr_operand(const uint16_t* tile, int ld, int row0, int col0,
+                                                  int lane) {
+  const int rsub = (lane >> 5) * 4 + ((lane & 15) >> 2);
+  const int csub = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const uint16_t* p = tile + (row0 + rsub) * ld + col0 + csub;
+  const s16x4 lo = ds_read_tr16(p);
+  const s16x4 hi = ds_read_tr16(p + 8 * ld);
+  const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+  const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+  uint4 v;
+  v.x = l2.x;
+  v.y = l2.y;
+  v.z = h2.x;
+  v.w = h2.y;
+  return as_bf16x8(v);
+}
+
 // Row r (0..31) of C register `reg` for lane group g.
 __device__ __forceinline__ int c_row(int reg, int g) { return (reg >> 2) * 8 + g * 4 + (reg & 3); }
 
+// Branch-free two-interval test: key in [cb, ce) or [db, de) (unsigned range compares).
 __device__ __forceinline__ bool interval_visible(int key, int cb, int ce, int db, int de) {
-  return (key >= cb && key < ce) || (key >= db && key < de);
+  const bool in_ctx = static_cast<uint32_t>(key - cb) < static_cast<uint32_t>(ce - cb);
+  const bool in_draft = static_cast<uint32_t>(key - db) < static_cast<uint32_t>(de - db);
+  return in_ctx | in_draft;
 }
+
+// Row-interval form used per tile: offsets relative to the tile's first key, so the per-element
+// test is two compares against values held in registers.
+struct RowIntervals {
+  int c0, cl, d0, dl;  // context start offset and length, draft start offset and length
+  __device__ __forceinline__ void at_tile(int key0, int cb, int ce, int db, int de) {
+    c0 = cb - key0;
+    cl = ce - cb;
+    d0 = db - key0;
+    dl = de - db;
+  }
+  __device__ __forceinline__ bool visible(int off) const {
+    return (static_cast<uint32_t>(off - c0) < static_cast<uint32_t>(cl)) |
+           (static_cast<uint32_t>(off - d0) < static_cast<uint32_t>(dl));
+  }
+};
 
 }  // namespace aspec

@@ -12,19 +12,22 @@ constexpr int kFwdTileN = 64;
 // Key-major kernel (dK/dV): tiles of kBwdTileM query rows x kBwdTileN keys.
 constexpr int kBwdTileM = 32;
 constexpr int kBwdTileN = 128;
+// dK/dV work units cover at most this many query tiles of one key tile.
+constexpr int kBwdChunk = 32;
+// List entries carry the tile index in the low bits and "full tile" in bit 31.
+constexpr uint32_t kFullBit = 0x80000000u;
 
 struct PlanView {
-  int64_t nmf, nnf, nmb, nnb;
+  int64_t nmf, nnf, nmb, nnb, max_units;
   int32_t* f_classes;
-  int32_t* f_pcnt;
-  int32_t* f_pidx;
-  int32_t* f_fcnt;
-  int32_t* f_fidx;
+  int32_t* f_cnt;     // [nmf] visible key tiles per query tile
+  int32_t* f_list;    // [nmf][nnf] ascending key tiles | kFullBit
   int32_t* b_classes;
-  int32_t* b_pcnt;
-  int32_t* b_pidx;
-  int32_t* b_fcnt;
-  int32_t* b_fidx;
+  int32_t* b_cnt;     // [nnb] visible query tiles per key tile
+  int32_t* b_list;    // [nnb][nmb] descending query tiles | kFullBit
+  int32_t* b_chunks;  // [nnb] work units of each key tile (>= 1)
+  int32_t* b_units;   // [max_units] (key tile << 16 | chunk), longest first
+  int32_t* b_nunits;  // [1]
   size_t bytes;
 };
 
@@ -34,6 +37,7 @@ inline PlanView plan_view(void* base, int64_t nq, int64_t nk) {
   p.nnf = (nk + kFwdTileN - 1) / kFwdTileN;
   p.nmb = (nq + kBwdTileM - 1) / kBwdTileM;
   p.nnb = (nk + kBwdTileN - 1) / kBwdTileN;
+  p.max_units = p.nnb * ((p.nmb + kBwdChunk - 1) / kBwdChunk + 1);
   int32_t* cur = static_cast<int32_t*>(base);
   size_t used = 0;
   auto take = [&](int64_t count) {
@@ -42,15 +46,14 @@ inline PlanView plan_view(void* base, int64_t nq, int64_t nk) {
     return out;
   };
   p.f_classes = take(p.nmf * p.nnf);
-  p.f_pcnt = take(p.nmf);
-  p.f_pidx = take(p.nmf * p.nnf);
-  p.f_fcnt = take(p.nmf);
-  p.f_fidx = take(p.nmf * p.nnf);
+  p.f_cnt = take(p.nmf);
+  p.f_list = take(p.nmf * p.nnf);
   p.b_classes = take(p.nmb * p.nnb);
-  p.b_pcnt = take(p.nnb);
-  p.b_pidx = take(p.nnb * p.nmb);
-  p.b_fcnt = take(p.nnb);
-  p.b_fidx = take(p.nnb * p.nmb);
+  p.b_cnt = take(p.nnb);
+  p.b_list = take(p.nnb * p.nmb);
+  p.b_chunks = take(p.nnb);
+  p.b_units = take(p.max_units);
+  p.b_nunits = take(1);
   p.bytes = used * sizeof(int32_t);
   return p;
 }

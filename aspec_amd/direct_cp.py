@@ -290,7 +290,7 @@ class _DSparkAttention(torch.autograd.Function):
         dk = torch.empty((1, nk, hkv, d), dtype=k.dtype, device=k.device)
         dv = torch.empty((1, nk, hkv, v.shape[-1]), dtype=v.dtype, device=v.device)
         size = ctypes.c_size_t()
-        _lib.call("aspec_dspark_attn_bwd_workspace_bytes", nq, hq, ctypes.byref(size))
+        _lib.call("aspec_dspark_attn_bwd_workspace_bytes", nq, nk, hq, hkv, ctypes.byref(size))
         workspace = torch.empty(size.value, dtype=torch.uint8, device=q.device)
         outv = out.transpose(1, 2)
         args = (
@@ -302,7 +302,8 @@ class _DSparkAttention(torch.autograd.Function):
             _lib.ptr(dv), dv.stride(1), dv.stride(2), _lib.ptr(workspace),
             _lib.stream_handle(q.device),
         )
-        for stage, name in ((1, "attn_bwd_prepare"), (2, "attn_bwd_dq"), (4, "attn_bwd_dkdv")):
+        for stage, name in ((1, "attn_bwd_prepare"), (2, "attn_bwd_dq"), (4, "attn_bwd_dkdv"),
+                            (8, "attn_bwd_finalize")):
             with _timing.region(name):
                 _lib.call("aspec_dspark_attn_bwd_stages", stage, *args)
         return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None, None, None

@@ -121,9 +121,12 @@ int aspec_dspark_attn_fwd(const void* q, int64_t q_stride_token, int64_t q_strid
                           float* lse, void* stream);
 
 /*
- * Workspace (bytes) needed by aspec_dspark_attn_bwd.
+ * Workspace (bytes) needed by aspec_dspark_attn_bwd: per-row delta and log2-scaled LSE
+ * ([Hq][Nq] fp32 each) and fp32 dK/dV accumulators ([K][Hkv][128] each) for key tiles whose
+ * query list is split over several work units.
  */
-int aspec_dspark_attn_bwd_workspace_bytes(int64_t num_queries, int64_t q_heads, size_t* bytes);
+int aspec_dspark_attn_bwd_workspace_bytes(int64_t num_queries, int64_t num_keys, int64_t q_heads,
+                                          int64_t kv_heads, size_t* bytes);
 
 /*
  * DSpark attention backward: dQ, dK, dV (bf16) from dO (bf16) and an optional dLSE (fp32 [Hq][Nq],
@@ -146,10 +149,12 @@ int aspec_dspark_attn_bwd(const void* q, int64_t q_stride_token, int64_t q_strid
 
 /*
  * The same backward, one stage at a time: `stages` is a bit mask of 1 = prepare
- * (delta = rowsum(dO*O) - dLSE and LSE*log2(e) into the workspace; the role of the reference's
- * preprocess launch, aspec/kernels/cutedsl/cudnn_gqa/preprocess.py:44-333), 2 = dQ, 4 = dK/dV
- * (the main launch, cudnn_gqa_backward.py:276-296). Stages run in that order; a later stage
- * needs the workspace an earlier call prepared on the same stream.
+ * (delta = rowsum(dO*O) - dLSE and LSE*log2(e) into the workspace, zeroed split-tile
+ * accumulators; the role of the reference's preprocess launch,
+ * aspec/kernels/cutedsl/cudnn_gqa/preprocess.py:44-333), 2 = dQ, 4 = dK/dV (the main launch,
+ * cudnn_gqa_backward.py:276-296), 8 = finalize (split-tile accumulators to bf16, the role of
+ * postprocess.py:38-581). Stages run in that order; a later stage needs the workspace an earlier
+ * call prepared on the same stream.
  */
 int aspec_dspark_attn_bwd_stages(int stages, const void* q, int64_t q_stride_token,
                                  int64_t q_stride_head, const void* k, int64_t k_stride_token,

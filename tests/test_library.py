@@ -34,8 +34,8 @@ def test_size_queries_and_error_codes_without_gpu():
     size = ctypes.c_size_t()
     assert lib.aspec_dspark_plan_bytes(8192, 12288, ctypes.byref(size)) == 0
     assert size.value > 0 and size.value % 256 == 0
-    assert lib.aspec_dspark_attn_bwd_workspace_bytes(8192, 32, ctypes.byref(size)) == 0
-    assert size.value == 2 * 8192 * 32 * 4
+    assert lib.aspec_dspark_attn_bwd_workspace_bytes(8192, 12288, 32, 8, ctypes.byref(size)) == 0
+    assert size.value == (2 * 8192 * 32 + 2 * 12288 * 8 * 128) * 4
     assert lib.aspec_loss_stats_floats() == 8
     # invalid geometry is rejected before any launch, with the reference's message
     with pytest.raises(ValueError, match="Invalid THD fixed sparse geometry"):
