@@ -601,11 +601,9 @@ __global__ void __launch_bounds__(kWave * kKvWaves) attn_bwd_dkdv_kernel(AttnArg
 
   for (int i = 0; i < iters; ++i) {
     const KvStage& s = st[i & 1];
-    if (static_cast<uint32_t>(list[first + i / a.group]) & kFullBit) {
-      dkdv_iter<false>(s, krow, vrow, dkacc, dvacc, ikey, a.scale_log2, c, g);
-    } else {
-      dkdv_iter<true>(s, krow, vrow, dkacc, dvacc, ikey, a.scale_log2, c, g);
-    }
+    // One masked code path: the per-row interval test is cheap next to this iteration's 32 MFMAs,
+    // and a single body keeps the accumulators' register assignment stable across the loop.
+    dkdv_iter<true>(s, krow, vrow, dkacc, dvacc, ikey, a.scale_log2, c, g);
     if (i + 1 < iters) put(st[(i + 1) & 1]);
     if (i + 2 < iters) fetch(i + 2);
     __syncthreads();
