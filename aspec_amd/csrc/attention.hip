@@ -19,8 +19,6 @@ namespace {
 
 constexpr int kTM = kFwdTileM;          // query rows per wave (one per lane column)
 constexpr int kTN = kFwdTileN;          // keys per tile
-constexpr int kVtLd = kTN + 4;          // transposed 64-key tile stride (136 B)
-constexpr int kQtLd = kBwdTileM + 4;    // transposed 32-row tile stride (72 B)
 constexpr int kMaxGroup = 8;
 constexpr int kKvWaves = kBwdTileN / 32;
 constexpr int kUnitChunkBits = 12;
@@ -92,27 +90,26 @@ struct TileLoader {
     }
   }
 
-  __device__ __forceinline__ void store(uint16_t* rm, uint16_t* tr, int t_ld, int tid) const {
+  // Writes the staged rows into the swizzled LDS tile `rm` (16 lanes cover one row's 16 chunks:
+  // conflict free).
+  __device__ __forceinline__ void store(uint16_t* rm, int tid) const {
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
       if (!active(tid, p)) continue;
       const int r = row_of(tid, p);
       const int col = col_of(tid, p);
-      if (rm) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(rm + (r + j) * kRowLd + col) = v[p][j];
-      }
-      if (tr) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          u32x2 w;
-          w.x = static_cast<uint32_t>(half_of(v[p][0], e)) | (static_cast<uint32_t>(half_of(v[p][1], e)) << 16);
-          w.y = static_cast<uint32_t>(half_of(v[p][2], e)) | (static_cast<uint32_t>(half_of(v[p][3], e)) << 16);
-          *reinterpret_cast<u32x2*>(tr + (col + e) * t_ld + r) = w;
-        }
-      }
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(rm + tile_chunk_off(r + j, col)) = v[p][j];
     }
   }
+};
+
+// A row-major operand in a swizzled LDS tile: this lane's row at `off` (row_operand_off), read
+// one 16-dim k-step at a time.
+struct RowOperand {
+  const uint16_t* tile;
+  int off;
+  __device__ __forceinline__ uint4 step(int ds) const { return load16(tile + (off ^ (ds << 4))); }
 };
 
 // Operand fragment of one row: 8 x 16 dims at g*8 of each 16-wide step (rows past the tensor are
@@ -132,24 +129,24 @@ __device__ __forceinline__ void load_row_frag(bf16x8 (&frag)[8], const uint16_t*
 #define ASPEC_STEP_FENCE() __builtin_amdgcn_sched_barrier(0)
 
 // Two independent 8-step chains: acc0 += A0 x B0, acc1 += A1 x B1 over the 128-dim reduction.
-// A rows live in LDS (row-major, `ra0` / `ra1` at this lane's row and g*8); the B operands come
-// from registers (`b0`, `b1`) or, when null, from LDS rows `rb0` / `rb1`.
-__device__ __forceinline__ void mfma_chains2(f32x16& acc0, f32x16& acc1, const uint16_t* ra0,
-                                             const uint16_t* ra1, const bf16x8* b0,
-                                             const bf16x8* b1, const uint16_t* rb0,
-                                             const uint16_t* rb1) {
+// A rows live in LDS (`ra0` / `ra1`); the B operands come from registers (`b0`, `b1`) or, when
+// null, from LDS rows `rb0` / `rb1`.
+__device__ __forceinline__ void mfma_chains2(f32x16& acc0, f32x16& acc1, const RowOperand& ra0,
+                                             const RowOperand& ra1, const bf16x8* b0,
+                                             const bf16x8* b1, const RowOperand& rb0,
+                                             const RowOperand& rb1) {
   acc0 = f32x16{};
   acc1 = f32x16{};
-  uint4 a0 = load16(ra0), a1 = load16(ra1);
-  uint4 x0 = b0 ? uint4{} : load16(rb0), x1 = b1 ? uint4{} : load16(rb1);
+  uint4 a0 = ra0.step(0), a1 = ra1.step(0);
+  uint4 x0 = b0 ? uint4{} : rb0.step(0), x1 = b1 ? uint4{} : rb1.step(0);
 #pragma unroll
   for (int ds = 0; ds < 8; ++ds) {
     uint4 na0{}, na1{}, nx0{}, nx1{};
     if (ds < 7) {
-      na0 = load16(ra0 + (ds + 1) * 16);
-      na1 = load16(ra1 + (ds + 1) * 16);
-      if (!b0) nx0 = load16(rb0 + (ds + 1) * 16);
-      if (!b1) nx1 = load16(rb1 + (ds + 1) * 16);
+      na0 = ra0.step(ds + 1);
+      na1 = ra1.step(ds + 1);
+      if (!b0) nx0 = rb0.step(ds + 1);
+      if (!b1) nx1 = rb1.step(ds + 1);
     }
     acc0 = mfma32(as_bf16x8(a0), b0 ? b0[ds] : as_bf16x8(x0), acc0);
     acc1 = mfma32(as_bf16x8(a1), b1 ? b1[ds] : as_bf16x8(x1), acc1);
@@ -166,16 +163,16 @@ __device__ __forceinline__ void mfma_chains2(f32x16& acc0, f32x16& acc1, const u
 // columns d*32 .. +32 = the output rows), read with transpose loads.
 template <int KS>
 __device__ __forceinline__ void mfma_tr_blocks(f32x16 (&acc)[4], const uint16_t* tile,
-                                               const bf16x8 (&b)[KS], int lane) {
+                                               const TrOffsets& tro, const bf16x8 (&b)[KS]) {
   bf16x8 cur[4];
 #pragma unroll
-  for (int d = 0; d < 4; ++d) cur[d] = read_tr_operand(tile, kRowLd, 0, d * 32, lane);
+  for (int d = 0; d < 4; ++d) cur[d] = read_tr_operand(tile, tro, 0, d * 32);
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     bf16x8 nxt[4];
     if (ks + 1 < KS) {
 #pragma unroll
-      for (int d = 0; d < 4; ++d) nxt[d] = read_tr_operand(tile, kRowLd, (ks + 1) * 16, d * 32, lane);
+      for (int d = 0; d < 4; ++d) nxt[d] = read_tr_operand(tile, tro, (ks + 1) * 16, d * 32);
     }
 #pragma unroll
     for (int d = 0; d < 4; ++d) acc[d] = mfma32(cur[d], b[ks], acc[d]);
@@ -200,14 +197,6 @@ __device__ __forceinline__ void store_row_c(uint16_t* dst, const f32x16 (&acc)[4
   }
 }
 
-__device__ __forceinline__ void atomic_add_row_c(float* dst, const f32x16 (&acc)[4], int g) {
-#pragma unroll
-  for (int db = 0; db < 4; ++db) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) atomicAdd(dst + db * 32 + c_row(r, g), acc[db][r]);
-  }
-}
-
 // ---------------------------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------------------------
@@ -215,10 +204,11 @@ template <bool PARTIAL>
 __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
                                          const bf16x8 (&qf)[8], f32x16 (&oacc)[4], float& m_run,
                                          float& l_run, const RowIntervals& iv, float scale_log2,
-                                         int c, int g) {
+                                         int ro, const TrOffsets& tro, int g) {
   f32x16 s[2];
-  mfma_chains2(s[0], s[1], sk + c * kRowLd + g * 8, sk + (32 + c) * kRowLd + g * 8, qf, qf,
-               nullptr, nullptr);
+  const RowOperand none{nullptr, 0};
+  mfma_chains2(s[0], s[1], RowOperand{sk, ro}, RowOperand{sk + 32 * kRowLd, ro}, qf, qf, none,
+               none);
   float tile_max = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
@@ -256,7 +246,7 @@ __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
   pb[1] = pack_c_half(s[0], 8);
   pb[2] = pack_c_half(s[1], 0);
   pb[3] = pack_c_half(s[1], 8);
-  mfma_tr_blocks<4>(oacc, sv, pb, g * 32 + c);
+  mfma_tr_blocks<4>(oacc, sv, tro, pb);
 }
 
 // One LDS buffer per workgroup (34 KB) with synchronous staging: two or more workgroups per CU
@@ -292,6 +282,8 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) {
   const uint16_t* vbase = a.v + hkv * a.vsh;
   const int count = a.plan.f_cnt[m];
   const int32_t* list = a.plan.f_list + m * a.plan.nnf;
+  const int ro = row_operand_off(c, g);
+  const TrOffsets tro(lane);
 
   for (int t = 0; t < count; ++t) {
     const uint32_t entry = static_cast<uint32_t>(list[t]);
@@ -301,18 +293,23 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) {
     {
       TileLoader<NT, kTN> tile;
       tile.load(kbase + key0 * a.kst, a.kst, valid, tid);
-      tile.store(s_k, nullptr, 0, tid);
+      tile.store(s_k, tid);
       tile.load(vbase + key0 * a.vst, a.vst, valid, tid);
-      tile.store(s_v, nullptr, 0, tid);
+      tile.store(s_v, tid);
     }
     __syncthreads();
+    int ro_t = ro;
+    TrOffsets tro_t = tro;
+    opaque(ro_t);
+    opaque(tro_t.lo);
+    opaque(tro_t.hi);
     if (entry & kFullBit) {
       RowIntervals iv{};
-      fwd_tile<false>(s_k, s_v, qf, oacc, m_run, l_run, iv, a.scale_log2, c, g);
+      fwd_tile<false>(s_k, s_v, qf, oacc, m_run, l_run, iv, a.scale_log2, ro_t, tro_t, g);
     } else {
       RowIntervals iv;
       iv.at_tile(static_cast<int>(key0), cb, ce, db, de);
-      fwd_tile<true>(s_k, s_v, qf, oacc, m_run, l_run, iv, a.scale_log2, c, g);
+      fwd_tile<true>(s_k, s_v, qf, oacc, m_run, l_run, iv, a.scale_log2, ro_t, tro_t, g);
     }
   }
 
@@ -389,13 +386,15 @@ template <bool PARTIAL>
 __device__ __forceinline__ void dq_tile(const uint16_t* sk, const uint16_t* sv,
                                         const bf16x8 (&qf)[8], const bf16x8 (&df)[8],
                                         f32x16 (&dqacc)[4], float lse2, float delta,
-                                        const RowIntervals& iv, float scale_log2, int c, int g) {
+                                        const RowIntervals& iv, float scale_log2, int ro,
+                                        const TrOffsets& tro, int g) {
   bf16x8 dsb[4];
+  const RowOperand none{nullptr, 0};
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     f32x16 s, dp;
-    mfma_chains2(s, dp, sk + (kb * 32 + c) * kRowLd + g * 8, sv + (kb * 32 + c) * kRowLd + g * 8,
-                 qf, df, nullptr, nullptr);
+    mfma_chains2(s, dp, RowOperand{sk + kb * 32 * kRowLd, ro}, RowOperand{sv + kb * 32 * kRowLd, ro},
+                 qf, df, none, none);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       float p = fast_exp2(s[r] * scale_log2 - lse2);
@@ -405,7 +404,7 @@ __device__ __forceinline__ void dq_tile(const uint16_t* sk, const uint16_t* sv,
     dsb[kb * 2 + 0] = pack_c_half(s, 0);
     dsb[kb * 2 + 1] = pack_c_half(s, 8);
   }
-  mfma_tr_blocks<4>(dqacc, sk, dsb, g * 32 + c);
+  mfma_tr_blocks<4>(dqacc, sk, tro, dsb);
 }
 
 template <int G>
@@ -443,6 +442,8 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
   const uint16_t* vbase = a.v + hkv * a.vsh;
   const int count = a.plan.f_cnt[m];
   const int32_t* list = a.plan.f_list + m * a.plan.nnf;
+  const int ro = row_operand_off(c, g);
+  const TrOffsets tro(lane);
 
   for (int t = 0; t < count; ++t) {
     const uint32_t entry = static_cast<uint32_t>(list[t]);
@@ -452,170 +453,361 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
     {
       TileLoader<NT, kTN> tile;
       tile.load(kbase + key0 * a.kst, a.kst, valid, tid);
-      tile.store(s_k, nullptr, 0, tid);
+      tile.store(s_k, tid);
       tile.load(vbase + key0 * a.vst, a.vst, valid, tid);
-      tile.store(s_v, nullptr, 0, tid);
+      tile.store(s_v, tid);
     }
     __syncthreads();
+    int ro_t = ro;
+    TrOffsets tro_t = tro;
     if (entry & kFullBit) {
       RowIntervals iv{};
-      dq_tile<false>(s_k, s_v, qf, df, dqacc, lse2, delta, iv, a.scale_log2, c, g);
+      dq_tile<false>(s_k, s_v, qf, df, dqacc, lse2, delta, iv, a.scale_log2, ro_t, tro_t, g);
     } else {
       RowIntervals iv;
       iv.at_tile(static_cast<int>(key0), cb, ce, db, de);
-      dq_tile<true>(s_k, s_v, qf, df, dqacc, lse2, delta, iv, a.scale_log2, c, g);
+      dq_tile<true>(s_k, s_v, qf, df, dqacc, lse2, delta, iv, a.scale_log2, ro_t, tro_t, g);
     }
   }
   if (valid_q) store_row_c(a.dq + qrow * a.dqst + head * a.dqsh, dqacc, a.scale, g);
 }
 
 // ---------------------------------------------------------------------------------------------
-// dK / dV: key-major. Each wave owns 32 keys of a 128-key tile. A work unit walks one chunk of the
-// (descending) list of query tiles that see its key tile and, inside each query tile, all G heads
-// of the KV group, so dK/dV are reduced over the GQA group in registers. A key tile covered by one
-// unit is written directly; one split over several units is accumulated in fp32 and finalized.
+// dK / dV: key-major. A workgroup owns one 128-key tile and walks one chunk of the (descending)
+// list of query tiles that see it; inside each query tile it visits all G heads of the KV group,
+// so dK/dV are reduced over the GQA group in registers. A key tile covered by one unit is written
+// directly; one split over several units is accumulated in fp32 and finalized.
+//
+// Eight waves in two roles share each 32-key slice w = wave % 4:
+//   P waves (0-3):  S = Q K^T (K slice in registers), P = exp2(S*scale*log2e - LSE2) masked,
+//                   P -> LDS, dV += P^T dO;
+//   dS waves (4-7): one iteration behind, dP = dO V^T (V slice in registers), dS = P (dP - delta)
+//                   with P from LDS, dK += dS^T Q.
+// The two waves of a SIMD thus overlap one's softmax VALU work with the other's MFMAs. Q/dO rows
+// and the row scalars cycle through four LDS stages: P waves work on stage i, dS waves on stage
+// i-1, stage i+1 is landing and stage i+2 is being loaded, straight from global memory into LDS
+// (global_load_lds_dwordx4: no staging registers), so every load has two iterations to arrive.
+// One barrier per iteration.
 // ---------------------------------------------------------------------------------------------
+constexpr int kDkdvWaves = 2 * kKvWaves;
+constexpr int kDkdvStages = 4;
+
 struct KvStage {
-  uint16_t q[kBwdTileM * kRowLd];
+  uint16_t q[kBwdTileM * kRowLd];     // swizzled rows
   uint16_t dout[kBwdTileM * kRowLd];
-  float lse2[kBwdTileM];
+  float lse2[kBwdTileM];               // lse2 and delta are filled by one 64-lane load
   float delta[kBwdTileM];
-  int4 ends[kBwdTileM];
+  int32_t ends[4][kBwdTileM];          // cb, ce, db, de of each row (two 64-lane loads)
+  uint32_t mask[kKvWaves][kBwdTileM];  // bit c of [w][row]: key 32w + c of the tile is visible
+};
+static_assert(offsetof(KvStage, delta) == offsetof(KvStage, lse2) + 4 * kBwdTileM, "layout");
+static_assert(offsetof(KvStage, ends) == offsetof(KvStage, delta) + 4 * kBwdTileM, "layout");
+
+// Direct global -> LDS loads (gfx950 global_load_lds_dword / _dwordx4): lane l's bytes land at
+// `lds_wave_base` + l * size; the base, which goes through M0, must be the same for the whole
+// wave. They are issued from inline assembly so the compiler's wait-count bookkeeping never sees
+// them: it would otherwise wait for every one of them before each LDS read and barrier, which
+// defeats loading two iterations ahead. Callers wait for them explicitly (vmcnt). The compiler's
+// own vector loads are issued before or after these and return in order, so its waits stay
+// correct (at worst they also cover these loads). M0 is written one instruction before its use.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) char*)(p))));
+}
+__device__ __forceinline__ void lds_load16(const void* src, void* lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_address(lds_wave_base)), "v"(src)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_load4(const void* src, void* lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(lds_address(lds_wave_base)), "v"(src)
+               : "memory", "m0");
+}
+
+// P of one iteration in C-register order: [slice][register quad][lane].
+struct PExchange {
+  f32x4 p[kKvWaves][4][kWave];
 };
 
-// krow / vrow: this lane's key row of the LDS-resident K and V tiles, at dim offset g*8.
-template <bool PARTIAL>
-__device__ __forceinline__ void dkdv_iter(const KvStage& s, const uint16_t* krow,
-                                          const uint16_t* vrow, f32x16 (&dkacc)[4],
-                                          f32x16 (&dvacc)[4], int ikey, float scale_log2, int c,
-                                          int g) {
-  // S = Q K^T and dP = dO V^T; C layout: lane <-> this wave's key, rows <-> queries.
-  f32x16 sacc, dp;
-  mfma_chains2(sacc, dp, s.q + c * kRowLd + g * 8, s.dout + c * kRowLd + g * 8, nullptr, nullptr,
-               krow, vrow);
+// Bits [lo, hi) of the 32-key word starting at `base`.
+__device__ __forceinline__ uint32_t interval_bits(int lo, int hi, int base) {
+  const int a = min(max(lo - base, 0), 32);
+  const int e = min(max(hi - base, 0), 32);
+  return e > a ? static_cast<uint32_t>((1ull << e) - (1ull << a)) : 0u;
+}
+
+// acc = A x B over the 128-dim reduction: A rows from LDS (all eight k-steps read up front), B
+// from registers.
+__device__ __forceinline__ f32x16 mfma_chain_lds_reg(const RowOperand& ra, const bf16x8 (&b)[8]) {
+  uint4 x[8];
+#pragma unroll
+  for (int ds = 0; ds < 8; ++ds) x[ds] = ra.step(ds);
+  f32x16 acc{};
+#pragma unroll
+  for (int ds = 0; ds < 8; ++ds) acc = mfma32(as_bf16x8(x[ds]), b[ds], acc);
+  return acc;
+}
+
+// acc[d] += A(d, ks) x B[ks] over a 32-row reduction (two k-steps), A read transposed from `tile`
+// (all eight fragments read up front).
+__device__ __forceinline__ void mfma_tr_32(f32x16 (&acc)[4], const uint16_t* tile,
+                                           const TrOffsets& tro, const bf16x8 (&b)[2]) {
+  bf16x8 x[2][4];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) x[ks][d] = read_tr_operand(tile, tro, ks * 16, d * 32);
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) acc[d] = mfma32(x[ks][d], b[ks], acc[d]);
+}
+
+// P wave: S, masked P (to LDS for the dS wave) and dV += P^T dO for one stage. Rows at or past
+// `valid` hold copies of a real row and get an empty mask. `key_base` is the slice's first key.
+__device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf16x8 (&kf)[8],
+                                            f32x16 (&dvacc)[4], float scale_log2, int w, int valid,
+                                            int key_base, int ro, const TrOffsets& tro, int lane) {
+  const int g = lane >> 5;
+  const int c = lane & 31;
+  if (lane < kBwdTileM) {  // visibility word of row `lane` for this slice
+    const uint32_t bits = interval_bits(s.ends[0][lane], s.ends[1][lane], key_base) |
+                          interval_bits(s.ends[2][lane], s.ends[3][lane], key_base);
+    s.mask[w][lane] = lane < valid ? bits : 0u;
+  }
+  __builtin_amdgcn_wave_barrier();
+  f32x16 sacc = mfma_chain_lds_reg(RowOperand{s.q, ro}, kf);  // rows: queries, lane: key
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq) {
     const int r0 = rq * 8 + g * 4;
     const f32x4 l4 = *reinterpret_cast<const f32x4*>(s.lse2 + r0);
-    const f32x4 d4 = *reinterpret_cast<const f32x4*>(s.delta + r0);
+    const u32x4 m4 = *reinterpret_cast<const u32x4*>(&s.mask[w][r0]);
+    f32x4 p4;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int r = rq * 4 + j;
-      float p = fast_exp2(sacc[r] * scale_log2 - l4[j]);
-      if (PARTIAL) {
-        const int4 e = s.ends[r0 + j];
-        p = interval_visible(ikey, e.x, e.y, e.z, e.w) ? p : 0.f;
-      }
-      sacc[r] = p;
-      dp[r] = p * (dp[r] - d4[j]);
+      const float p = fast_exp2(sacc[rq * 4 + j] * scale_log2 - l4[j]);
+      const int keep = __builtin_amdgcn_sbfe(static_cast<int>(m4[j]), c, 1);  // 0 or -1
+      p4[j] = __int_as_float(__float_as_int(p) & keep);
+      sacc[rq * 4 + j] = p4[j];
     }
+    px.p[w][rq][lane] = p4;
   }
   const bf16x8 pp[2] = {pack_c_half(sacc, 0), pack_c_half(sacc, 8)};
-  const bf16x8 dd[2] = {pack_c_half(dp, 0), pack_c_half(dp, 8)};
-  mfma_tr_blocks<2>(dvacc, s.dout, pp, g * 32 + c);
-  mfma_tr_blocks<2>(dkacc, s.q, dd, g * 32 + c);
+  mfma_tr_32(dvacc, s.dout, tro, pp);
 }
 
-__global__ void __launch_bounds__(kWave * kKvWaves) attn_bwd_dkdv_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) KvStage st[2];
-  __shared__ __attribute__((aligned(16))) uint16_t s_key[kBwdTileN * kRowLd];
-  __shared__ __attribute__((aligned(16))) uint16_t s_val[kBwdTileN * kRowLd];
-  // An AGPR operand anywhere in the kernel makes instruction selection emit the AGPR form of the
-  // MFMAs, so the dK/dV accumulators stay in AGPRs across the walk instead of being copied in
-  // and out of VGPRs every iteration.
-  asm volatile("" ::"a"(0));
+// dS wave: dP, dS = P (dP - delta) and dK += dS^T Q for one stage.
+__device__ __forceinline__ void dkdv_ds_step(const KvStage& s, const PExchange& px,
+                                             const bf16x8 (&vf)[8], f32x16 (&dkacc)[4], int w,
+                                             int ro, const TrOffsets& tro, int lane) {
+  const int g = lane >> 5;
+  f32x16 dp = mfma_chain_lds_reg(RowOperand{s.dout, ro}, vf);
+#pragma unroll
+  for (int rq = 0; rq < 4; ++rq) {
+    const int r0 = rq * 8 + g * 4;
+    const f32x4 d4 = *reinterpret_cast<const f32x4*>(s.delta + r0);
+    const f32x4 p4 = px.p[w][rq][lane];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dp[rq * 4 + j] = p4[j] * (dp[rq * 4 + j] - d4[j]);
+  }
+  const bf16x8 dd[2] = {pack_c_half(dp, 0), pack_c_half(dp, 8)};
+  mfma_tr_32(dkacc, s.q, tro, dd);
+}
+
+// LDS of the dK/dV kernel: the stage ring and P exchange during the walk, then, for the epilogue,
+// one 32-key x 128-dim fp32 tile per key slice.
+struct DkdvShared {
+  union {
+    struct {
+      KvStage st[kDkdvStages];
+      PExchange px[2];
+    } walk;
+    float out[kKvWaves][kBwdTileM * kHeadDim];
+  };
+};
+
+// Epilogue of one wave: its 32 keys x 128 dims (C layout: lane = key, registers = dims) pass
+// through the LDS tile `t` (row = key; 16-byte chunk j of row k stored at chunk j ^ k, which keeps
+// both the writes and the row reads bank-conflict free) so that every global write instruction
+// covers one contiguous key row: a bf16 store of the whole row (direct) or two fp32 atomic adds
+// of 64 consecutive dims each (key tiles split over several units).
+__device__ __forceinline__ void dkdv_store(const f32x16 (&acc)[4], float* t, int64_t key_first,
+                                           int64_t nk, bool direct, uint16_t* dst,
+                                           int64_t dst_stride, float* ws, int64_t ws_stride,
+                                           float mul, int lane) {
+  const int g = lane >> 5;
+  const int c = lane & 31;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int chunk = db * 8 + rq * 2 + g;  // dims db*32 + rq*8 + g*4 .. +3
+      const f32x4 v = {acc[db][rq * 4 + 0], acc[db][rq * 4 + 1], acc[db][rq * 4 + 2],
+                       acc[db][rq * 4 + 3]};
+      *reinterpret_cast<f32x4*>(t + c * kHeadDim + ((chunk ^ c) << 2)) = v;
+    }
+  __builtin_amdgcn_wave_barrier();
+  for (int k = 0; k < kBwdTileM; ++k) {
+    const int64_t key = key_first + k;
+    if (key >= nk) break;
+    const float* row = t + k * kHeadDim;
+    if (direct) {
+      const f32x2_t v = *reinterpret_cast<const f32x2_t*>(row + (((lane >> 1) ^ k) << 2) + (lane & 1) * 2);
+      *reinterpret_cast<uint32_t*>(dst + key * dst_stride + 2 * lane) = pack_bf16x2(v[0] * mul, v[1] * mul);
+    } else {
+      const float v0 = row[(((lane >> 2) ^ k) << 2) + (lane & 3)];
+      const float v1 = row[(((16 + (lane >> 2)) ^ k) << 2) + (lane & 3)];
+      atomicAdd(ws + key * ws_stride + lane, v0);
+      atomicAdd(ws + key * ws_stride + 64 + lane, v1);
+    }
+  }
+}
+
+// s_waitcnt immediates: at most `n` vector-memory loads of this wave outstanding / all LDS
+// operations of this wave complete (the other counters left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+constexpr int kLgkmcnt0 = 0xF | (0x3 << 14) | (0x7 << 4);
+
+// Workgroup barrier for LDS traffic this wave has already waited for. Unlike __syncthreads() it
+// does not wait for outstanding global -> LDS loads (the caller waits for the ones it needs with
+// vmcnt). The wavefront-scope fences emit nothing; they keep the compiler from moving memory
+// operations across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) DkdvShared sh;
+  KvStage& st0 = sh.walk.st[0];
+  KvStage& st1 = sh.walk.st[1];
+  KvStage& st2 = sh.walk.st[2];
+  KvStage& st3 = sh.walk.st[3];
+  PExchange& px0 = sh.walk.px[0];
+  PExchange& px1 = sh.walk.px[1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool p_role = wave < kKvWaves;
+  const int w = wave % kKvWaves;
   const int g = lane >> 5;
   const int c = lane & 31;
   const int hkv = blockIdx.x % a.hkv;
   const int64_t u = blockIdx.x / a.hkv;
   if (u >= a.plan.b_nunits[0]) return;
-  const int32_t unit = a.plan.b_units[u];
+  const int32_t unit = __builtin_amdgcn_readfirstlane(a.plan.b_units[u]);
   const int64_t n = unit >> kUnitChunkBits;
   const int chunk = unit & ((1 << kUnitChunkBits) - 1);
-  const int count = a.plan.b_cnt[n];
+  const int count = __builtin_amdgcn_readfirstlane(a.plan.b_cnt[n]);
   const int first = chunk * kBwdChunk;
   const int last = min(count, first + kBwdChunk);
   const int iters = max(0, last - first) * a.group;
   const int32_t* list = a.plan.b_list + n * a.plan.nmb;
+  const int64_t key0 = n * kBwdTileN;
+  // The unit's (at most 32) query tiles, one per lane, read with readlane in the loop: no memory
+  // access there besides the stage loads.
+  const int my_tile = lane < last - first ? list[first + lane] & ~kFullBit : 0;
 
-  const int64_t key = n * kBwdTileN + wave * 32 + c;
+  // This wave's B operand for the whole walk: K (P waves) or V (dS waves) rows of its 32 keys.
+  const int64_t key = key0 + w * 32 + c;
   const bool valid_k = key < a.nk;
-  {
-    // The unit's 128 keys of K and V stay in LDS for the whole walk (keys past K are zero).
-    const int64_t key0 = n * kBwdTileN;
-    const int valid = static_cast<int>(min<int64_t>(kBwdTileN, a.nk - key0));
-    TileLoader<kWave * kKvWaves, kBwdTileN> tile;
-    tile.load(a.k + key0 * a.kst + hkv * a.ksh, a.kst, valid, tid);
-    tile.store(s_key, nullptr, 0, tid);
-    tile.load(a.v + key0 * a.vst + hkv * a.vsh, a.vst, valid, tid);
-    tile.store(s_val, nullptr, 0, tid);
-  }
-  const uint16_t* krow = s_key + (wave * 32 + c) * kRowLd + g * 8;
-  const uint16_t* vrow = s_val + (wave * 32 + c) * kRowLd + g * 8;
-  f32x16 dkacc[4] = {};
-  f32x16 dvacc[4] = {};
-  const int ikey = static_cast<int>(key);
+  const int64_t ksafe = valid_k ? key : a.nk - 1;
+  bf16x8 kvf[8];
+  load_row_frag(kvf, p_role ? a.k + ksafe * a.kst + hkv * a.ksh : a.v + ksafe * a.vst + hkv * a.vsh,
+                valid_k, g);
+  f32x16 acc[4] = {};
+  const int ro = row_operand_off(c, g);
+  const TrOffsets tro(lane);
 
-  // Staging roles: threads [0,128) Q rows, [128,256) dO rows, [0,32) also the row scalars.
-  TileLoader<128, kBwdTileM> rows;
-  float sc_lse2 = 0.f, sc_delta = 0.f;
-  int4 sc_ends = make_int4(0, 0, 0, 0);
-  const bool loads_q = tid < 128;
-  const int rtid = loads_q ? tid : tid - 128;
-  auto fetch = [&](int i) {
-    const int64_t q0 = static_cast<int64_t>(list[first + i / a.group] & ~kFullBit) * kBwdTileM;
-    const int head = hkv * a.group + i % a.group;
-    const int valid = static_cast<int>(min<int64_t>(kBwdTileM, a.nq - q0));
-    if (loads_q) rows.load(a.q + q0 * a.qst + head * a.qsh, a.qst, valid, rtid);
-    else rows.load(a.dout + q0 * a.dost + head * a.dosh, a.dost, valid, rtid);
-    if (tid < kBwdTileM) {
-      const bool ok = tid < valid;
-      const int64_t qr = q0 + (ok ? tid : valid - 1);
-      const int64_t idx = static_cast<int64_t>(head) * a.nq + qr;
-      sc_lse2 = ok ? a.ws_lse2[idx] : 0.f;
-      sc_delta = ok ? a.ws_delta[idx] : 0.f;
-      const int4 e = make_int4(a.ends[1 * a.nq + qr], a.ends[2 * a.nq + qr], a.ends[3 * a.nq + qr],
-                               a.ends[4 * a.nq + qr]);
-      sc_ends = ok ? e : make_int4(0, 0, 0, 0);
+  // Loads of iteration `it` into a stage. Wave v moves Q and dO rows 4v .. 4v+3 (lane l lands at
+  // physical chunk l % 16 of row 4v + l / 16, so it fetches the logical chunk swizzled there);
+  // rows past the tensor repeat its last row. Waves 0-2 also move the row scalars.
+  const int lrow = wave * 4 + (lane >> 4);
+  const int lcol = ((lane & 15) ^ swz(lrow)) * 8;
+  const bool three_loads = wave < 3;
+  auto row_base = [&](int it, int64_t& q0, int& head, int& valid) {
+    q0 = static_cast<int64_t>(__builtin_amdgcn_readlane(my_tile, it / a.group)) * kBwdTileM;
+    head = hkv * a.group + it % a.group;
+    valid = static_cast<int>(min<int64_t>(kBwdTileM, a.nq - q0));
+  };
+  auto issue = [&](int it, KvStage& sb) {
+    int64_t q0;
+    int head, valid;
+    row_base(it, q0, head, valid);
+    const int64_t qr = q0 + min(lrow, valid - 1);
+    lds_load16(a.q + qr * a.qst + head * a.qsh + lcol, sb.q + wave * 4 * kRowLd);
+    lds_load16(a.dout + qr * a.dost + head * a.dosh + lcol, sb.dout + wave * 4 * kRowLd);
+    const int64_t r = q0 + min(lane & 31, valid - 1);
+    const int hi = lane >> 5;
+    if (wave == 0) {  // lanes 0-31: lse2, lanes 32-63: delta
+      lds_load4((hi ? a.ws_delta : a.ws_lse2) + static_cast<int64_t>(head) * a.nq + r, sb.lse2);
+    } else if (wave < 3) {  // endpoints 1,2 (wave 1) and 3,4 (wave 2)
+      const int e = (wave - 1) * 2;
+      lds_load4(a.ends + static_cast<int64_t>(e + hi + 1) * a.nq + r, sb.ends[e]);
     }
   };
-  auto put = [&](KvStage& s) {
-    if (loads_q) rows.store(s.q, nullptr, 0, rtid);
-    else rows.store(s.dout, nullptr, 0, rtid);
-    if (tid < kBwdTileM) {
-      s.lse2[tid] = sc_lse2;
-      s.delta[tid] = sc_delta;
-      s.ends[tid] = sc_ends;
-    }
+  auto wait_loads = [&](bool ahead) {
+    if (!ahead) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    else if (three_loads) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2));
   };
-  if (iters > 0) {
-    fetch(0);
-    put(st[0]);
-    if (iters > 1) fetch(1);
-  }
-  __syncthreads();
+  if (iters > 0) issue(0, st0);
+  if (iters > 1) issue(1, st1);
+  wait_loads(iters > 1);
+  lds_barrier();
 
-  for (int i = 0; i < iters; ++i) {
-    const KvStage& s = st[i & 1];
-    // One masked code path: the per-row interval test is cheap next to this iteration's 32 MFMAs,
-    // and a single body keeps the accumulators' register assignment stable across the loop.
-    dkdv_iter<true>(s, krow, vrow, dkacc, dvacc, ikey, a.scale_log2, c, g);
-    if (i + 1 < iters) put(st[(i + 1) & 1]);
-    if (i + 2 < iters) fetch(i + 2);
-    __syncthreads();
+  // Trip i (stage ring position K = i % 4): P waves on stage i, dS waves on stage i-1, loads of
+  // iteration i+2 into stage i+2.
+  auto trip = [&](auto kc, int i, KvStage& s_cur, KvStage& s_prv, KvStage& s_ld, PExchange& x_cur,
+                  PExchange& x_prv) {
+    const bool ahead = i + 2 < iters;
+    if (ahead) issue(i + 2, s_ld);
+    int ro_t = ro;
+    TrOffsets tro_t = tro;
+    opaque(ro_t);
+    opaque(tro_t.lo);
+    opaque(tro_t.hi);
+    if (p_role) {
+      if (i < iters) {
+        int64_t q0;
+        int head, valid;
+        row_base(i, q0, head, valid);
+        dkdv_p_step(s_cur, x_cur, kvf, acc, a.scale_log2, w, valid,
+                    static_cast<int>(key0) + w * 32, ro_t, tro_t, lane);
+      }
+    } else if (i > 0) {
+      dkdv_ds_step(s_prv, x_prv, kvf, acc, w, ro_t, tro_t, lane);
+    }
+    wait_loads(ahead);  // this wave's part of stage i+1 has landed
+    lds_barrier();
+    (void)kc;
+  };
+  for (int i = 0; i <= iters; i += 4) {
+    trip(0, i, st0, st3, st2, px0, px1);
+    if (i + 1 > iters) break;
+    trip(1, i + 1, st1, st0, st3, px1, px0);
+    if (i + 2 > iters) break;
+    trip(2, i + 2, st2, st1, st0, px0, px1);
+    if (i + 3 > iters) break;
+    trip(3, i + 3, st3, st2, st1, px1, px0);
   }
-  if (!valid_k) return;
-  if (a.plan.b_chunks[n] == 1) {
-    store_row_c(a.dk + key * a.dkst + hkv * a.dksh, dkacc, a.scale, g);
-    store_row_c(a.dv + key * a.dvst + hkv * a.dvsh, dvacc, 1.f, g);
-  } else {
-    atomic_add_row_c(a.ws_dk + (key * a.hkv + hkv) * kHeadDim, dkacc, g);
-    atomic_add_row_c(a.ws_dv + (key * a.hkv + hkv) * kHeadDim, dvacc, g);
-  }
+  // Epilogue in the walk's LDS (every load has landed): P waves (dV) first, then dS waves (dK).
+  const bool direct = a.plan.b_chunks[n] == 1;
+  const int64_t ws_stride = static_cast<int64_t>(a.hkv) * kHeadDim;
+  const int64_t key_first = key0 + w * 32;
+  if (p_role)
+    dkdv_store(acc, sh.out[w], key_first, a.nk, direct, a.dv + hkv * a.dvsh, a.dvst,
+               a.ws_dv + hkv * kHeadDim, ws_stride, 1.f, lane);
+  lds_barrier();
+  if (!p_role)
+    dkdv_store(acc, sh.out[w], key_first, a.nk, direct, a.dk + hkv * a.dksh, a.dkst,
+               a.ws_dk + hkv * kHeadDim, ws_stride, a.scale, lane);
 }
 
 int validate(const AttnArgs& a, int64_t head_dim) {
@@ -760,7 +952,7 @@ extern "C" int aspec_dspark_attn_bwd_stages(
   }
   if (stages & 4) {
     hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(static_cast<uint32_t>(a.plan.max_units * a.hkv)),
-                       dim3(kWave * kKvWaves), 0, s, a);
+                       dim3(kWave * kDkdvWaves), 0, s, a);
     if ((rc = check_launch("attn_bwd_dkdv_kernel"))) return rc;
   }
   if (stages & 8) {

@@ -1,5 +1,5 @@
-// Building blocks shared by the DSpark attention kernels: tile staging into LDS (row-major and
-// transposed) and the MFMA 32x32x16 bf16 operand conventions.
+// Building blocks shared by the DSpark attention kernels: the swizzled LDS tile layout and the
+// MFMA 32x32x16 bf16 operand conventions.
 //
 // MFMA convention used throughout (v_mfma_f32_32x32x16_bf16, wave64):
 //   lane l = 32*g + c (g = lane group 0/1, c = column 0..31);
@@ -7,6 +7,8 @@
 //   B operand: lane supplies column c, the same reduction slots (g, e);
 //   C/D: lane holds column c, register r <-> row (r/4)*8 + g*4 + (r%4).
 // Only C's layout is interpreted; for A and B only the pairing of equal (g, e) slots matters.
+// Row-major operands put slot (g, e) of k-step ds at dim 16*ds + 8*g + e; transposed operands and
+// packed C halves put it at reduction row (e/4)*8 + g*4 + e%4 of the 16-row k-step.
 #pragma once
 
 #include "common.h"
@@ -14,7 +16,35 @@
 namespace aspec {
 
 constexpr int kHeadDim = 128;
-constexpr int kRowLd = kHeadDim + 8;  // row-major tile stride (bf16), 272 B: conflict-free b128 reads
+constexpr int kRowLd = kHeadDim;  // LDS tile row: 128 bf16 = 256 B, unpadded
+
+// LDS tiles hold rows of 128 bf16 as 16 chunks of 16 B; logical chunk j of row r is stored at
+// chunk j ^ swz(r). swz is built so that every LDS read pattern used here is bank-conflict free,
+// for 64 banks (256 B per cycle) and for 32 (128 B per cycle):
+//  * row reads (ds_read_b128, lane c reads row c, all lanes the same logical chunk): swz is a
+//    bijection on r % 16, and its low three bits a bijection on r % 8;
+//  * transpose reads (ds_read_b64_tr_b16, 4 consecutive rows x 4 adjacent chunks per 32 lanes,
+//    4 rows x 2 chunks per 16 lanes): bits 2-3 and bits 1-2 of swz are bijections on r % 4.
+// With r = b3 b2 b1 b0: swz = (b1 ^ b3, b0, b1, b2).
+__device__ __forceinline__ int swz(int row) {
+  return ((row >> 2) & 1) | (row & 2) | ((row & 1) << 2) | ((((row >> 1) ^ (row >> 3)) & 1) << 3);
+}
+
+// Element offset of (row, dims col .. col+7) in a swizzled tile (col % 8 == 0).
+__device__ __forceinline__ int tile_chunk_off(int row, int col) {
+  return row * kRowLd + (((col >> 3) ^ swz(row)) << 3);
+}
+
+// Hides a value's origin from the optimizer (emits no instruction). Applied to the lane offsets
+// inside a tile loop, it keeps the per-step swizzled addresses (one XOR each) from being hoisted
+// out of the loop into a register apiece.
+__device__ __forceinline__ void opaque(int& x) { asm volatile("" : "+v"(x)); }
+
+// Element offset of this lane's row-major operand read at k-step 0 (dims 8*g .. 8*g+7 of `row`).
+// The read of k-step ds (dims 16*ds + 8*g ..) is at row_operand_off(row, g) ^ (ds << 4).
+__device__ __forceinline__ int row_operand_off(int row, int g) {
+  return row * kRowLd + ((g ^ swz(row)) << 3);
+}
 
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -28,27 +58,14 @@ __device__ __forceinline__ uint4 load16(const uint16_t* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
+// bf16 element e (0..7) of a 16-byte chunk.
 __device__ __forceinline__ uint16_t half_of(const uint4& v, int e) {
   const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
   return static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
 }
 
-// Reads an A/B operand whose 8 reduction slots live as two runs of 4 contiguous bf16:
-// slots e<4 at p[g*4 + e], slots e>=4 at p[8 + g*4 + e-4].
-__device__ __forceinline__ bf16x8 read_split_operand(const uint16_t* p, int g) {
-  const u32x2 lo = *reinterpret_cast<const u32x2*>(p + g * 4);
-  const u32x2 hi = *reinterpret_cast<const u32x2*>(p + 8 + g * 4);
-  uint4 v;
-  v.x = lo.x;
-  v.y = lo.y;
-  v.z = hi.x;
-  v.w = hi.y;
-  return as_bf16x8(v);
-}
-
 // Packs C registers [base, base+8) into the bf16 operand whose slot e pairs with C row
-// (e/4)*8 + g*4 + e%4 of the 16-row half starting at base/8*16 -- the slot order read_split_operand
-// expects from the other operand.
+// (e/4)*8 + g*4 + e%4 of the 16-row half starting at base/8*16.
 __device__ __forceinline__ bf16x8 pack_c_half(const f32x16& c, int base) {
   uint4 v;
   v.x = pack_bf16x2(c[base + 0], c[base + 1]);
@@ -58,46 +75,6 @@ __device__ __forceinline__ bf16x8 pack_c_half(const f32x16& c, int base) {
   return as_bf16x8(v);
 }
 
-// Stages `rows` rows x 128 dims of a strided [row][head][dim] bf16 tensor into LDS.
-//   row_major: dst_rm[r * kRowLd + d]          (may be null)
-//   transposed: dst_t[d * t_ld + r]            (may be null; rows must be a multiple of 4)
-// Rows at or beyond `limit` are zero-filled. Work items are 4 rows x 8 dims, spread over
-// `nthreads` threads starting at `tid`.
-__device__ __forceinline__ void stage_tile(const uint16_t* __restrict__ src, int64_t row_stride,
-                                           int64_t first_row, int64_t limit, int rows,
-                                           uint16_t* dst_rm, uint16_t* dst_t, int t_ld, int tid,
-                                           int nthreads) {
-  const int items = (rows / 4) * (kHeadDim / 8);
-  for (int it = tid; it < items; it += nthreads) {
-    const int rg = it / (kHeadDim / 8);
-    const int dc = it - rg * (kHeadDim / 8);
-    uint4 v[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t row = first_row + rg * 4 + j;
-      if (row < limit) {
-        v[j] = load16(src + row * row_stride + dc * 8);
-      } else {
-        v[j] = make_uint4(0, 0, 0, 0);
-      }
-    }
-    if (dst_rm) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        *reinterpret_cast<uint4*>(dst_rm + (rg * 4 + j) * kRowLd + dc * 8) = v[j];
-    }
-    if (dst_t) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        u32x2 w;
-        w.x = static_cast<uint32_t>(half_of(v[0], e)) | (static_cast<uint32_t>(half_of(v[1], e)) << 16);
-        w.y = static_cast<uint32_t>(half_of(v[2], e)) | (static_cast<uint32_t>(half_of(v[3], e)) << 16);
-        *reinterpret_cast<u32x2*>(dst_t + (dc * 8 + e) * t_ld + rg * 4) = w;
-      }
-    }
-  }
-}
-
 typedef __attribute__((ext_vector_type(4))) short s16x4;
 
 __device__ __forceinline__ s16x4 ds_read_tr16(const uint16_t* p) {
@@ -105,20 +82,31 @@ __device__ __forceinline__ s16x4 ds_read_tr16(const uint16_t* p) {
       (__attribute__((address_space(3))) s16x4*)(__attribute__((address_space(3))) void*)p);
 }
 
-// A operand whose rows are the columns of a row-major LDS tile (a transposed fragment), read with
-// gfx950's transpose load ds_read_b64_tr_b16. Within each 16-lane group, lane i receives element
-// i%4 of the 8-byte chunks that lanes i/4, i/4+4, i/4+8 and i/4+12 of its group address. Lane s
-// therefore addresses row rsub(s) = (s/32)*4 + (s%16)/4 and columns csub(s) = 16*((s/16)%2) +
-// 4*(s%4) .. +3, and lane L = 32g + i ends up holding column col0 + i of rows
-// row0 + {g*4 + e} (e < 4, first read) and row0 + {8 + g*4 + e-4} (second read): exactly the
-// (g, e) reduction slots read_split_operand() / pack_c_half() use.
-__device__ __forceinline__ bf16x8 read_tr_operand(const uint16_t* tile, int ld, int row0, int col0,
-                                                  int lane) {
-  const int rsub = (lane >> 5) * 4 + ((lane & 15) >> 2);
-  const int csub = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  const uint16_t* p = tile + (row0 + rsub) * ld + col0 + csub;
-  const s16x4 lo = ds_read_tr16(p);
-  const s16x4 hi = ds_read_tr16(p + 8 * ld);
+// Transposed A operands read from a row-major swizzled tile with gfx950's transpose load
+// ds_read_b64_tr_b16. Within each 16-lane group, lane i receives element i%4 of the 8-byte pieces
+// that lanes i/4, i/4+4, i/4+8 and i/4+12 of its group address. Lane s therefore addresses row
+// rsub(s) = (s/32)*4 + (s%16)/4 and columns csub(s) = 16*((s/16)%2) + 4*(s%4) .. +3, and lane
+// L = 32g + i ends up holding column col0 + i of rows row0 + {g*4 + e} (e < 4, first read) and
+// row0 + {8 + g*4 + e-4} (second read): the (g, e) slots pack_c_half() produces.
+// `lo` / `hi` are this lane's element offsets for row0 = 0, col0 = 0; they hold for any row0 that
+// is a multiple of 16 (swz depends on row % 16 only) and any col0 that is a multiple of 32
+// (col0 / 8 only flips chunk bits 2-3, which the lane's own chunk bits 0-1 do not touch).
+struct TrOffsets {
+  int lo, hi;
+  __device__ __forceinline__ explicit TrOffsets(int lane) {
+    const int rsub = (lane >> 5) * 4 + ((lane & 15) >> 2);
+    const int csub = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    lo = rsub * kRowLd + (((csub >> 3) ^ swz(rsub)) << 3) + (csub & 7);
+    hi = (rsub + 8) * kRowLd + (((csub >> 3) ^ swz(rsub + 8)) << 3) + (csub & 7);
+  }
+};
+
+// Transposed fragment: rows row0 .. row0+15 (the reduction; row0 % 16 == 0), columns
+// col0 .. col0+31 (the MFMA rows; col0 % 32 == 0).
+__device__ __forceinline__ bf16x8 read_tr_operand(const uint16_t* tile, const TrOffsets& o,
+                                                  int row0, int col0) {
+  const s16x4 lo = ds_read_tr16(tile + row0 * kRowLd + (o.lo ^ col0));
+  const s16x4 hi = ds_read_tr16(tile + row0 * kRowLd + (o.hi ^ col0));
   const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
   const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
   uint4 v;
