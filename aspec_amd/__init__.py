@@ -1,10 +1,19 @@
 """aspec_amd: MI355X-native (gfx950 HIP) DSpark draft hot path.
 
 Drop-in replacements for the reference operators of aspec/models/ops (direct CP / THD attention,
-THD sparse metadata, tiled L1, the selective-head losses) backed by hand-written HIP kernels in
-libaspec_amd.so, reached through the C ABI of include/aspec_amd.h.
+THD sparse metadata, tiled L1, the selective-head losses), the packing collator
+(aspec/data/utils.py), the anchor layout (anchors.py), output-block compaction (output_blocks.py)
+and the DSpark targets (dspark.py), backed by hand-written HIP kernels in libaspec_amd.so,
+reached through the C ABI of include/aspec_amd.h.
 """
 
+from aspec_amd.anchors import (  # noqa: F401
+    document_anchor_slots,
+    sample_anchor_positions,
+    sample_document_anchor_positions,
+    validate_injected_anchors,
+)
+from aspec_amd.collate import DFlashPackingCollator  # noqa: F401
 from aspec_amd.direct_cp import (  # noqa: F401
     MASK_VALUE,
     DirectCPMetadata,
@@ -13,11 +22,33 @@ from aspec_amd.direct_cp import (  # noqa: F401
     direct_cp_attention_from_kv,
     direct_cp_attention_observation,
 )
+from aspec_amd.targets import decay_weights, dspark_targets  # noqa: F401
+from aspec_amd.output_blocks import (  # noqa: F401
+    output_block_counts,
+    output_block_indices,
+    owner_block_indices,
+    prepare_block_layout,
+    restore_blocks,
+    select_blocks,
+)
 from aspec_amd.thd_attention import thd_fa4_attention  # noqa: F401
 from aspec_amd.thd_sparse_metadata import build_thd_sparse_pair  # noqa: F401
 from aspec_amd.tiled_l1 import tiled_l1_from_logits  # noqa: F401
 
 __all__ = [
+    "DFlashPackingCollator",
+    "decay_weights",
+    "document_anchor_slots",
+    "dspark_targets",
+    "output_block_counts",
+    "output_block_indices",
+    "owner_block_indices",
+    "prepare_block_layout",
+    "restore_blocks",
+    "sample_anchor_positions",
+    "sample_document_anchor_positions",
+    "select_blocks",
+    "validate_injected_anchors",
     "MASK_VALUE",
     "DirectCPMetadata",
     "build_context_positions",

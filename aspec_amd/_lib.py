@@ -58,9 +58,26 @@ SIGNATURES = {
     "aspec_ce_l1_bwd": (
         _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64] + [_c_void_p] * 5
     ),
+    "aspec_pack_copy": (_int, [_c_void_p, _i64, _c_void_p]),
+    "aspec_pack_row_metadata": (_int, [_c_void_p, _i64, _i64] + [_c_void_p] * 4),
+    "aspec_sample_document_anchors": (
+        _int, [_c_void_p, _int, _c_void_p, _i64, _c_void_p] + [_i64] * 5 + [_c_void_p] * 5
+    ),
+    "aspec_sample_anchors": (
+        _int, [_c_void_p, _int, _c_void_p, _int] + [_i64] * 5 + [_c_void_p] * 5
+    ),
+    "aspec_validate_injected_anchors": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _int, _c_void_p] + [_i64] * 4
+        + [_int, _c_void_p, _c_void_p, _c_void_p]
+    ),
+    "aspec_output_block_layout": (_int, [_c_void_p] + [_i64] * 6 + [_c_void_p] * 3),
+    "aspec_dspark_targets": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p] + [_i64] * 5
+        + [_c_void_p] * 8
+    ),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib = None
@@ -108,6 +125,17 @@ def check(status: int) -> None:
 def call(name: str, *args) -> None:
     lib = load()
     check(getattr(lib, name)(*args))
+
+
+# ASPEC_MASK_* dtype codes of include/aspec_amd.h
+def mask_dtype_code(tensor) -> int:
+    import torch
+
+    codes = {torch.float32: 0, torch.int64: 1, torch.int32: 2, torch.bool: 3, torch.uint8: 3,
+             torch.bfloat16: 4, torch.float16: 5}
+    if tensor.dtype not in codes:
+        raise ValueError(f"unsupported mask dtype {tensor.dtype}")
+    return codes[tensor.dtype]
 
 
 def ptr(tensor) -> int | None:

@@ -7,7 +7,11 @@ One step = one packed 4096-token row through the draft hot path, inputs resident
      the frozen-teacher table = target_hidden[4096, 4096] @ W^T (no grad),
   4. fused CE + softmax-L1 (HIP, indexed teacher rows), objective (0.1 CE + 0.9 L1) weighted by the
      DSpark eval mask x exp(-k/4) decay, normalised by the weight sum,
-  5. backward: dlogits (HIP), dO = dlogits @ W (hipBLASLt), attention backward (HIP).
+  5. backward: dlogits (HIP), dO = dlogits @ W (hipBLASLt), attention backward (HIP);
+  before the head: injected-anchor validation, output-block counts and the DSpark targets (labels,
+  eval mask, decay weights) from the anchors (HIP).
+Row-level operations that run once per row outside the step (packing collator, document anchor
+sampler) are timed separately and reported with "outside_step": true.
 Metric: input context tokens per second (4096 per step / wall time), as the reference's draft-only
 benchmark defines it (tools/performance/torchspec_benchmark.py:688,764).
 
@@ -79,17 +83,8 @@ def build_inputs(device, seed):
         "head": randn(VOCAB, HIDDEN, scale=0.02),
         "target_hidden": randn(w.context_length, HIDDEN),
     }
-    ids = torch.randint(0, VOCAB, (w.context_length,), generator=g)
-    anchors = torch.as_tensor(w.anchors)
-    B = w.block_size
-    label = anchors[:, None] + torch.arange(1, B + 1)[None]            # dspark.py:240-246
-    valid = label < w.sequence_length
-    safe = label.clamp(max=w.sequence_length - 1)
-    eval_mask = (valid & torch.as_tensor(w.keep)[:, None]).int().cumprod(-1).float()
-    decay = torch.exp(-torch.arange(B).float() / DECAY_GAMMA)           # dspark.py:163-172
-    x["targets"] = ids[safe].reshape(-1).to(device)
-    x["weights"] = (eval_mask * decay).reshape(-1).to(device)
-    x["teacher_index"] = (safe - 1).clamp(min=0).reshape(-1).to(device)  # dspark.py:381-383
+    x["input_ids"] = torch.randint(0, VOCAB, (1, w.context_length), generator=g).to(device)
+    x["loss_mask"] = torch.ones(1, w.context_length, dtype=torch.long, device=device)
     t = lambda a, dt: torch.as_tensor(a, dtype=dt, device=device)[None]  # noqa: E731
     x["meta_tensors"] = (t(w.anchors, torch.long), t(w.keep, torch.bool), t(w.context_positions, torch.long),
                          t(w.ctx_doc_ids, torch.long), t(w.anchor_doc_ids, torch.long))
@@ -127,11 +122,29 @@ def step(x, head_fn):
     import torch
 
     from aspec_amd import _timing
+    from aspec_amd.anchors import validate_injected_anchors
     from aspec_amd.direct_cp import DirectCPMetadata, direct_cp_attention_from_kv
+    from aspec_amd.targets import dspark_targets
     from aspec_amd.loss import ce_l1_from_logits
+    from aspec_amd.output_blocks import output_block_counts
 
     w = x["w"]
     anchors, keep, pos, docs, adocs = x["meta_tensors"]
+    # The frozen-teacher table depends on neither the anchors nor the draft: queued first, it keeps
+    # the GPU busy while the host waits on the validation and output-block transfers below.
+    with torch.no_grad(), _timing.region("teacher_gemm"):
+        teacher = torch.matmul(x["target_hidden"], x["head"].t())
+    # the configs inject their anchors (dflash.py:297-306): validated, then the output-block
+    # counts of the compacted head (dspark.py:347-352) and the labels / eval mask / decay weights
+    # (dspark.py:240-272, 311-315, 325)
+    anchors, keep = validate_injected_anchors(anchors, keep, loss_mask=x["loss_mask"],
+                                              num_anchors=w.num_blocks, block_size=w.block_size,
+                                              ctx_doc_ids=docs)
+    counts = output_block_counts(keep, w.num_blocks)
+    if sum(counts) != w.num_blocks:
+        raise RuntimeError("config anchors are all kept")
+    targets = dspark_targets(anchors, keep, x["input_ids"], x["loss_mask"], w.block_size,
+                             loss_decay_gamma=DECAY_GAMMA, ctx_doc_ids=docs)
     meta = DirectCPMetadata(anchors, keep, pos, w.block_size, 0, 1, None, context_doc_ids=docs,
                             anchor_doc_ids=adocs, sequence_length=w.sequence_length)
     for name in ("q", "k", "v"):
@@ -139,10 +152,9 @@ def step(x, head_fn):
     out, _ = direct_cp_attention_from_kv(x["q"], x["k"], x["v"], meta)
     hidden = out.transpose(1, 2).reshape(w.num_queries, w.q_heads * w.head_dim)
     logits = head_fn.apply(hidden, x["head"])
-    with torch.no_grad(), _timing.region("teacher_gemm"):
-        teacher = torch.matmul(x["target_hidden"], x["head"].t())
-    ce, l1 = ce_l1_from_logits(logits, x["targets"], teacher, teacher_indices=x["teacher_index"])
-    wts = x["weights"]
+    ce, l1 = ce_l1_from_logits(logits, targets.target_ids.reshape(-1), teacher,
+                               teacher_indices=targets.teacher_index.reshape(-1))
+    wts = targets.weights.reshape(-1)
     loss = (CE_ALPHA * (ce * wts).sum() + L1_ALPHA * (l1 * wts).sum()) / wts.sum().clamp(min=1e-6)
     loss.backward()
     return loss
@@ -169,12 +181,61 @@ def kernel_work(w):
         "loss_bwd": ("hbm", 3 * rows * VOCAB * 2),
         "thd_row_metadata": ("hbm", w.num_blocks * 17 + ctx * 16 + rows * 4 * 4 + w.num_keys * 4 * 4 + rows * 5 * 4),
         "attn_plan_build": ("hbm", rows * 5 * 4 * 2),
+        # anchors + keep in, masked anchors out, two loss-mask and two doc reads per kept anchor
+        "anchor_validate": ("hbm", w.num_blocks * (8 + 1 + 8 + 2 * 8 + 2 * 8)),
+        "output_block_layout": ("hbm", w.num_blocks + 8),
+        # per slot: ids, mask, docs reads (8 B each) and six outputs (4 x int64 + 2 x fp32)
+        "dspark_targets": ("hbm", w.num_blocks * 17 + rows * (3 * 8 + 4 * 8 + 2 * 4)),
     }
 
 
 _REGION_KERNEL = {"attn_fwd": "attn_fwd_kernel", "attn_bwd_dq": "attn_bwd_dq_kernel",
                   "attn_bwd_dkdv": "attn_bwd_dkdv_kernel", "attn_bwd_prepare": "attn_bwd_pre_kernel",
                   "loss_fwd": "void loss_fwd_resident<4>", "loss_bwd": "void loss_bwd_kernel<true>"}
+
+
+def aux_rows(device, w, reps):
+    """Row-level operations that run once per packed row, outside the draft step: the packing
+    collator on the config-2 row (one 4096-token document with 3 x 4096 target hidden states and
+    4096 last hidden states, bf16, plus ids and loss mask) and the document anchor sampler
+    (512 anchors, block 16). Returns {region: (mean_ms, launches, algorithmic bytes)}."""
+    import torch
+
+    from aspec_amd import _timing
+    from aspec_amd.anchors import sample_document_anchor_positions
+    from aspec_amd.collate import DFlashPackingCollator
+
+    T = w.context_length
+    g = torch.Generator(device=device).manual_seed(1)
+    feat = {"input_ids": torch.randint(0, VOCAB, (1, T), device=device, generator=g),
+            "loss_mask": torch.ones(1, T, dtype=torch.long, device=device),
+            "hidden_states": torch.randn(1, T, 3 * HIDDEN, device=device, generator=g).to(torch.bfloat16),
+            "last_hidden_states": torch.randn(1, T, HIDDEN, device=device, generator=g).to(torch.bfloat16),
+            "_aspec_work": {"execution_id": "bench"}}
+    collator = DFlashPackingCollator(T)
+    gen = torch.Generator(device=device).manual_seed(2)
+
+    def once():
+        batch = collator([feat])
+        sample_document_anchor_positions(batch["loss_mask"], batch["ctx_doc_ids"],
+                                         batch["packed_document_lengths"], w.num_blocks,
+                                         w.block_size, generator=gen)
+
+    for _ in range(3):
+        once()
+    torch.cuda.synchronize()
+    _timing.reset()
+    _timing.enable(True)
+    for _ in range(reps):
+        once()
+    torch.cuda.synchronize()
+    _timing.enable(False)
+    stats = _timing.summary()
+    moved = sum(feat[k].numel() * feat[k].element_size() for k in
+                ("input_ids", "loss_mask", "hidden_states", "last_hidden_states"))
+    work = {"pack_row": 2 * moved + T * 8 * 3,                 # read + write every field, 3 metadata rows
+            "anchor_sample": T * (8 + 8 + 4) + w.num_blocks * 9}  # mask, docs, compacted list; outputs
+    return {k: (stats[k]["mean_ms"], stats[k]["launches"], work[k]) for k in work if k in stats}
 
 
 def measured_traffic(region):
@@ -296,6 +357,11 @@ def main():
             gbs = amount / (stats["mean_ms"] * 1e-3) / 1e9
             entry.update(gbs=round(gbs, 1), frac_hbm=round(gbs / PEAK_HBM_GBS, 4))
         per_kernel[name] = entry
+    if not args.no_kernel_timing:
+        for name, (ms, launches, amount) in aux_rows(device, w, args.steps).items():
+            gbs = amount / (ms * 1e-3) / 1e9
+            per_kernel[name] = {"mean_ms": round(ms, 4), "launches": launches, "gbs": round(gbs, 1),
+                                "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "outside_step": True}
     roofline = None
     if kernels:
         dominant = max(kernels, key=lambda n: kernels[n]["total_ms"])

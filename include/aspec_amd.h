@@ -199,6 +199,125 @@ int aspec_ce_l1_bwd(const void* logits, const void* teacher, const int64_t* teac
                     int64_t vocab, const float* stats, const float* grad_l1, const float* grad_ce,
                     void* grad_logits, void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Row-level operations around the attention and loss: packing, anchors, output blocks, targets.
+ * ------------------------------------------------------------------------------------------- */
+
+/* dtype codes of loss / attention mask inputs. */
+#define ASPEC_MASK_F32 0
+#define ASPEC_MASK_I64 1
+#define ASPEC_MASK_I32 2
+#define ASPEC_MASK_U8 3 /* bool */
+#define ASPEC_MASK_BF16 4
+#define ASPEC_MASK_F16 5
+
+/* One copy of a packed-row build: `bytes` bytes from `src` to `dst`; src == NULL zero-fills. */
+typedef struct AspecCopySpan {
+  const void* src;
+  void* dst;
+  int64_t bytes;
+} AspecCopySpan;
+
+/*
+ * Executes `count` copy spans (a device array; destinations must not overlap) in one launch, one
+ * workgroup per span, 16-byte vectors where src, dst and size allow.
+ * Replaces the concatenation and padding copies of DFlashPackingCollator.__call__
+ * (aspec/data/utils.py:226-323): input_ids, loss_mask, hidden_states, last_hidden_states.
+ */
+int aspec_pack_copy(const AspecCopySpan* spans, int64_t count, void* stream);
+
+/*
+ * Per-token metadata of one packed row from cu_seqlens (int32 [num_docs + 1], device,
+ * cu_seqlens[0] = 0, non-decreasing, cu_seqlens[num_docs] = used tokens <= row_length):
+ *   ctx_doc_ids[t] = d where cu_seqlens[d] <= t < cu_seqlens[d+1], -1 on padding;
+ *   base_position_ids[t] = t - cu_seqlens[d], 0 on padding;
+ *   attention_mask[t] = t < used.
+ * All int64 [row_length]; any may be NULL.
+ * Replaces aspec/data/utils.py:263-285 (doc_ids, positions, attention_mask).
+ */
+int aspec_pack_row_metadata(const int32_t* cu_seqlens, int64_t num_docs, int64_t row_length,
+                            int64_t* ctx_doc_ids, int64_t* base_position_ids,
+                            int64_t* attention_mask, void* stream);
+
+/*
+ * Document anchor sampler for one packed row: sample_document_anchor_positions with
+ * _candidates and document_anchor_slots (aspec/models/ops/anchors.py:31-53,119-194).
+ *   loss_mask [seq_len] (ASPEC_MASK_* dtype), ctx_doc_ids int64 [seq_len],
+ *   document_lengths int64 [num_docs] (device), uniform float32 [num_docs]: the torch.rand draws
+ *   of anchors.py:180 (the phase is trunc(uniform * max(count, 1)) in float32);
+ *   total_slots / padded_slots as document_anchor_slots computes them (host), total_slots > 0;
+ *   workspace int32 [seq_len].
+ * Outputs anchors int64 [padded_slots], keep uint8 [padded_slots]. num_docs <= 4096.
+ */
+int aspec_sample_document_anchors(const void* loss_mask, int mask_dtype, const int64_t* ctx_doc_ids,
+                                  int64_t seq_len, const int64_t* document_lengths,
+                                  int64_t num_docs, int64_t num_anchors, int64_t block_size,
+                                  int64_t total_slots, int64_t padded_slots, const float* uniform,
+                                  int32_t* workspace, int64_t* anchors, uint8_t* keep,
+                                  void* stream);
+
+/*
+ * Per-sample anchor sampler: sample_anchor_positions (aspec/models/ops/anchors.py:197-266) for
+ * `batch` rows of seq_len > block_size tokens. loss_mask [batch][seq_len]; attention_mask may be
+ * NULL (else [batch][seq_len], ASPEC_MASK_* dtype attn_dtype); max_gap >= 0; uniform float32
+ * [batch] (the draws of anchors.py:260); workspace int32 [batch][seq_len].
+ * Outputs anchors int64 [batch][num_anchors], keep uint8 [batch][num_anchors].
+ */
+int aspec_sample_anchors(const void* loss_mask, int mask_dtype, const void* attention_mask,
+                         int attn_dtype, int64_t batch, int64_t seq_len, int64_t num_anchors,
+                         int64_t block_size, int64_t max_gap, const float* uniform,
+                         int32_t* workspace, int64_t* anchors, uint8_t* keep, void* stream);
+
+/*
+ * Injected-anchor validation: validate_injected_anchors (aspec/models/ops/anchors.py:77-116).
+ * anchors int64 / keep uint8 [batch][num_anchors]; loss_mask [batch][seq_len]; ctx_doc_ids int64
+ * [batch][seq_len] or NULL. Writes anchors_out = keep ? anchors : 0 and ORs into *status_flags
+ * (caller-zeroed): 1 a kept anchor without an in-bounds first target, 2 a kept anchor or its first
+ * target unsupervised, 4 a kept block crossing a document boundary, 8 some anchor kept.
+ */
+int aspec_validate_injected_anchors(const int64_t* anchors, const uint8_t* keep,
+                                    const void* loss_mask, int mask_dtype,
+                                    const int64_t* ctx_doc_ids, int64_t batch, int64_t seq_len,
+                                    int64_t num_anchors, int64_t block_size,
+                                    int allow_partial_last_target, int64_t* anchors_out,
+                                    int32_t* status_flags, void* stream);
+
+/*
+ * Output-block layout over keep uint8 [batch][slots], slots = owners * width:
+ *   order int64 [batch][slots] (may be NULL): inside each (row, owner) the slots with keep set in
+ *     original order, then the others in original order, as global slot indices (the stable
+ *     descending argsort of output_blocks.py:48 / 71, offset by owner * width);
+ *   summary int32 [1 + num_chunks]: summary[0] = max over rows and owners of the kept count;
+ *     summary[1 + c] = max over rows of the kept count in slots
+ *     [chunk_begin + c * chunk_size, min(chunk_begin + (c + 1) * chunk_size, chunk_end)),
+ *     num_chunks = ceil((chunk_end - chunk_begin) / chunk_size).
+ * Replaces output_block_counts / output_block_indices / owner_block_indices /
+ * prepare_block_layout (aspec/models/ops/output_blocks.py:19-98).
+ */
+int aspec_output_block_layout(const uint8_t* keep, int64_t batch, int64_t slots, int64_t owners,
+                              int64_t chunk_begin, int64_t chunk_end, int64_t chunk_size,
+                              int64_t* order, int32_t* summary, void* stream);
+
+/*
+ * DSpark labels, eval mask and decay weights (aspec/models/dspark.py:240-272, 311-315, 325):
+ * for block j of row b with anchor a and slot k < block_size,
+ *   label = a + 1 + k, valid = label < seq_len (and same document as the anchor if ctx_doc_ids),
+ *   label_index = keep ? min(label, seq_len - 1) : 0,
+ *   eval_mask = cumprod_k(keep & valid & loss_mask[label_index] > 0.5) * (k >= prediction_start),
+ *   weights = eval_mask * decay[k]   (decay float32 [block_size], as _decay_weights computes it),
+ *   target_ids = input_ids[label_index], prev_ids = (input_ids[a], target_ids[k-1]),
+ *   teacher_index = max(label_index - 1, 0).
+ * anchors int64 (in [0, seq_len)) / keep uint8 [batch][num_blocks]; input_ids int64, loss_mask,
+ * ctx_doc_ids (int64, may be NULL) [batch][seq_len]. Outputs [batch][num_blocks][block_size]; any
+ * may be NULL.
+ */
+int aspec_dspark_targets(const int64_t* anchors, const uint8_t* keep, const int64_t* input_ids,
+                         const void* loss_mask, int mask_dtype, const int64_t* ctx_doc_ids,
+                         int64_t batch, int64_t seq_len, int64_t num_blocks, int64_t block_size,
+                         int64_t prediction_start, const float* decay, int64_t* label_index,
+                         int64_t* target_ids, int64_t* prev_ids, int64_t* teacher_index,
+                         float* eval_mask, float* weights, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
