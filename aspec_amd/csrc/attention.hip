@@ -9,8 +9,8 @@
 // (S^T = K Q^T) so each lane owns one query row: the softmax statistics are per-lane scalars and
 // P^T feeds the P.V MFMA straight from registers.
 //
-// Tile loops are software pipelined: the global loads of the next tile are in flight in registers
-// while the current tile is computed from LDS.
+// Tile loops are software pipelined: the next tile streams from global memory straight into LDS
+// while the current one is computed.
 #include "attn_common.h"
 #include "plan.h"
 
@@ -48,60 +48,6 @@ struct AttnArgs {
   uint16_t* dq; int64_t dqst, dqsh;
   uint16_t* dk; int64_t dkst, dksh;
   uint16_t* dv; int64_t dvst, dvsh;
-};
-
-// Register-staged tile of ROWS rows x 128 dims, split into 4-row x 8-dim items over NT threads.
-// load() issues the global reads of rows [0, valid) of the tile (rows past `valid` are read
-// clamped and zeroed: no divergent branches); store() writes the row-major and/or transposed LDS
-// copies.
-template <int NT, int ROWS>
-struct TileLoader {
-  static constexpr int kItems = ROWS / 4 * (kHeadDim / 8);
-  static constexpr int kPer = (kItems + NT - 1) / NT;
-  static constexpr bool kEven = kItems % NT == 0;
-  uint4 v[kPer][4];
-
-  __device__ __forceinline__ static bool active(int tid, int p) { return kEven || tid + p * NT < kItems; }
-  __device__ __forceinline__ static int row_of(int tid, int p) { return (tid + p * NT) / 16 * 4; }
-  __device__ __forceinline__ static int col_of(int tid, int p) { return ((tid + p * NT) % 16) * 8; }
-
-  __device__ __forceinline__ void load(const uint16_t* __restrict__ base, int64_t stride, int valid,
-                                       int tid) {
-    if (valid >= ROWS) {
-#pragma unroll
-      for (int p = 0; p < kPer; ++p) {
-        if (!active(tid, p)) continue;
-        const uint16_t* ptr = base + row_of(tid, p) * stride + col_of(tid, p);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[p][j] = load16(ptr + j * stride);
-      }
-    } else {
-#pragma unroll
-      for (int p = 0; p < kPer; ++p) {
-        if (!active(tid, p)) continue;
-        const int r = row_of(tid, p);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int rr = min(r + j, valid - 1);
-          const uint4 x = load16(base + rr * stride + col_of(tid, p));
-          v[p][j] = r + j < valid ? x : make_uint4(0, 0, 0, 0);
-        }
-      }
-    }
-  }
-
-  // Writes the staged rows into the swizzled LDS tile `rm` (16 lanes cover one row's 16 chunks:
-  // conflict free).
-  __device__ __forceinline__ void store(uint16_t* rm, int tid) const {
-#pragma unroll
-    for (int p = 0; p < kPer; ++p) {
-      if (!active(tid, p)) continue;
-      const int r = row_of(tid, p);
-      const int col = col_of(tid, p);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(rm + tile_chunk_off(r + j, col)) = v[p][j];
-    }
-  }
 };
 
 // A row-major operand in a swizzled LDS tile: this lane's row at `off` (row_operand_off), read
@@ -197,30 +143,146 @@ __device__ __forceinline__ void store_row_c(uint16_t* dst, const f32x16 (&acc)[4
   }
 }
 
+// Direct global -> LDS loads (gfx950 global_load_lds_dword / _dwordx4): lane l's bytes land at
+// `lds_wave_base` + l * size; the base, which goes through M0, must be the same for the whole
+// wave. They are issued from inline assembly so the compiler's wait-count bookkeeping never sees
+// them: it would otherwise wait for every one of them before each LDS read and barrier, which
+// defeats loading two iterations ahead. Callers wait for them explicitly (vmcnt). The compiler's
+// own vector loads are issued before or after these and return in order, so its waits stay
+// correct (at worst they also cover these loads). M0 is written one instruction before its use.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) char*)(p))));
+}
+__device__ __forceinline__ void lds_load16(const void* src, void* lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_address(lds_wave_base)), "v"(src)
+               : "memory", "m0");
+}
+// Same, addressed as a wave-uniform 64-bit base (SGPRs) plus a 32-bit per-lane byte offset.
+__device__ __forceinline__ void lds_load16_at(const void* base, uint32_t byte_off, void* lds_wave_base) {
+  // readfirstlane returns int: go through uint32_t so the low word is zero-extended, not
+  // sign-extended into the high word.
+  const uint64_t b = reinterpret_cast<uintptr_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
+  const uint64_t sbase = static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds_address(lds_wave_base)), "v"(byte_off), "s"(sbase)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_load4(const void* src, void* lds_wave_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(lds_address(lds_wave_base)), "v"(src)
+               : "memory", "m0");
+}
+
+
+// s_waitcnt immediates: at most `n` vector-memory loads of this wave outstanding / all LDS
+// operations of this wave complete (the other counters left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+constexpr int kLgkmcnt0 = 0xF | (0x3 << 14) | (0x7 << 4);
+
+// Workgroup barrier for LDS traffic this wave has already waited for. Unlike __syncthreads() it
+// does not wait for outstanding global -> LDS loads (the caller waits for the ones it needs with
+// vmcnt). The wavefront-scope fences emit nothing; they keep the compiler from moving memory
+// operations across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+
+// K/V tile ring of the query-major kernels (forward, dQ): two stages, each a 64-key K tile and V
+// tile in swizzled rows, filled straight from global memory (no staging registers). Stage t+1 is
+// loading while stage t is computed; one wait and one barrier per tile.
+struct KvStageFwd {
+  uint16_t k[kTN * kRowLd];
+  uint16_t v[kTN * kRowLd];
+};
+
+// Issues this wave's share of the loads of the key tile at key0 into `st`: 32 wave-wide loads of
+// four rows each (16 for K, 16 for V), wave w taking loads w, w+G, ... Load i fills physical rows
+// 4(i%16) + l/16 (lane l at physical chunk l%16), so lane l fetches the logical chunk stored
+// there: (l%16) ^ swz(row). With row % 16 = 4q + s (q = i%4, s = l/16), swz(row) = swz(s) ^ T(q),
+// T(q) = (q&1) | (q&2)<<2, so the per-lane part `lane_chunk` = (l%16 ^ swz(s)) * 16 bytes is fixed
+// and each load costs one xor with a wave-uniform value. The tile base lives in SGPRs and the
+// per-lane offset is 32-bit (rows x stride < 2^31 is checked on the host). Keys past the tensor
+// repeat its last row (such tiles are always partial: the mask drops them).
+struct KvTileLanes {
+  uint32_t lane_chunk;  // (l%16 ^ swz(l/16)) * 16
+  int rsub;             // l / 16
+  __device__ __forceinline__ explicit KvTileLanes(int lane)
+      : lane_chunk(static_cast<uint32_t>(((lane & 15) ^ swz(lane >> 4)) << 4)), rsub(lane >> 4) {}
+};
+
+template <int G>
+__device__ __forceinline__ void issue_kv_tile(const uint16_t* kbase, int64_t kst,
+                                              const uint16_t* vbase, int64_t vst, int key0,
+                                              int nk, KvStageFwd& st, int wave,
+                                              const KvTileLanes& ln) {
+  const uint16_t* ktile = kbase + static_cast<int64_t>(key0) * kst;
+  const uint16_t* vtile = vbase + static_cast<int64_t>(key0) * vst;
+  const int last = min(nk - 1 - key0, kTN - 1);  // rows past it repeat it
+  const uint32_t kst2 = static_cast<uint32_t>(kst * 2), vst2 = static_cast<uint32_t>(vst * 2);
+#pragma unroll
+  for (int p = 0; p < (32 + G - 1) / G; ++p) {
+    const int i = wave + p * G;
+    if (i >= 32) break;
+    const int q = i & 3;
+    const uint32_t chunk = ln.lane_chunk ^ static_cast<uint32_t>(((q & 1) | ((q & 2) << 2)) << 4);
+    const int row = min((i & 15) * 4 + ln.rsub, last);
+    const uint32_t off = static_cast<uint32_t>(row) * (i < 16 ? kst2 : vst2) + chunk;
+    uint16_t* dst = (i < 16 ? st.k : st.v) + (i & 15) * 4 * kRowLd;
+    lds_load16_at(i < 16 ? ktile : vtile, off, dst);
+  }
+}
+
+// The plan list of one query tile, 64 entries at a time in one VGPR (lane j: entry base + j), read
+// with readlane: no memory access (and so no wait on the in-flight tile loads) inside the loop.
+struct ListWindow {
+  const int32_t* list;
+  int count, base, reg;
+  __device__ __forceinline__ void load(int b, int lane) {
+    base = b;
+    reg = b + lane < count ? list[b + lane] : 0;
+  }
+  __device__ __forceinline__ uint32_t entry(int t) const {
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(reg, t - base));
+  }
+};
+
 // ---------------------------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------------------------
-template <bool PARTIAL>
 __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
                                          const bf16x8 (&qf)[8], f32x16 (&oacc)[4], float& m_run,
-                                         float& l_run, const RowIntervals& iv, float scale_log2,
+                                         float& l_run, bool partial, const RowIntervals& iv, float scale_log2,
                                          int ro, const TrOffsets& tro, int g) {
   f32x16 s[2];
   const RowOperand none{nullptr, 0};
   mfma_chains2(s[0], s[1], RowOperand{sk, ro}, RowOperand{sk + 32 * kRowLd, ro}, qf, qf, none,
                none);
+  // Row maximum of the raw scores (scale > 0 commutes with max); the scale then folds into the
+  // exponent: p = exp2(s * scale*log2e - m).
+  if (partial) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] = iv.visible(kb * 32 + c_row(r, g)) ? s[kb][r] : -INFINITY;
+  }
   float tile_max = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float x = s[kb][r] * scale_log2;
-      if (PARTIAL) x = iv.visible(kb * 32 + c_row(r, g)) ? x : -INFINITY;
-      s[kb][r] = x;
-      tile_max = fmaxf(tile_max, x);
-    }
+    for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s[kb][r]);
   }
-  tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+  tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32)) * scale_log2;
   const bool grow = tile_max > m_run + kRescaleThreshold;
   if (__any(grow)) {
     const float m_new = grow ? tile_max : m_run;
@@ -230,12 +292,13 @@ __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
 #pragma unroll
     for (int d = 0; d < 4; ++d) oacc[d] *= alpha;
   }
+  const float neg_m = -m_run;
   float rowsum = 0.f;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float p = fast_exp2(s[kb][r] - m_run);
+      const float p = fast_exp2(fmaf(s[kb][r], scale_log2, neg_m));
       s[kb][r] = p;
       rowsum += p;
     }
@@ -249,17 +312,16 @@ __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
   mfma_tr_blocks<4>(oacc, sv, tro, pb);
 }
 
-// One LDS buffer per workgroup (34 KB) with synchronous staging: two or more workgroups per CU
-// hide each other's load latency, which pays more than register prefetch at this register budget.
+// Two K/V stages (64 KB) per workgroup, two workgroups per CU: the next tile streams into LDS
+// while this one is computed, and the two workgroups overlap each other's MFMA and softmax work.
 template <int G>
 __global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) {
-  constexpr int NT = kWave * G;
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[kTN * kRowLd];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v[kTN * kRowLd];
+  __shared__ __attribute__((aligned(16))) KvStageFwd ring[2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(wave >= 0 && wave < G);
   const int g = lane >> 5;
   const int c = lane & 31;
   const int hkv = blockIdx.x % a.hkv;
@@ -268,6 +330,18 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) {
   const int64_t qrow = m * kTM + c;
   const bool valid_q = qrow < a.nq;
   const int64_t qsafe = valid_q ? qrow : a.nq - 1;
+
+  const uint16_t* kbase = a.k + hkv * a.ksh;
+  const uint16_t* vbase = a.v + hkv * a.vsh;
+  const int nk = static_cast<int>(a.nk);
+  ListWindow lw{a.plan.f_list + m * a.plan.nnf, a.plan.f_cnt[m], 0, 0};
+  lw.load(0, lane);
+  const KvTileLanes lanes(lane);
+  auto issue = [&](uint32_t entry, int stage) {
+    const int key0 = static_cast<int>(entry & ~kFullBit) * kTN;
+    issue_kv_tile<G>(kbase, a.kst, vbase, a.vst, key0, nk, ring[stage], wave, lanes);
+  };
+  if (lw.count > 0) issue(lw.entry(0), 0);
 
   bf16x8 qf[8];
   load_row_frag(qf, a.q + qsafe * a.qst + head * a.qsh, valid_q, g);
@@ -278,39 +352,28 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) {
   f32x16 oacc[4] = {};
   float m_run = kMaskValue;
   float l_run = 0.f;
-  const uint16_t* kbase = a.k + hkv * a.ksh;
-  const uint16_t* vbase = a.v + hkv * a.vsh;
-  const int count = a.plan.f_cnt[m];
-  const int32_t* list = a.plan.f_list + m * a.plan.nnf;
   const int ro = row_operand_off(c, g);
   const TrOffsets tro(lane);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  lds_barrier();
 
-  for (int t = 0; t < count; ++t) {
-    const uint32_t entry = static_cast<uint32_t>(list[t]);
-    const int64_t key0 = static_cast<int64_t>(entry & ~kFullBit) * kTN;
-    const int valid = static_cast<int>(min<int64_t>(kTN, a.nk - key0));
-    __syncthreads();
-    {
-      TileLoader<NT, kTN> tile;
-      tile.load(kbase + key0 * a.kst, a.kst, valid, tid);
-      tile.store(s_k, tid);
-      tile.load(vbase + key0 * a.vst, a.vst, valid, tid);
-      tile.store(s_v, tid);
+  for (int t = 0; t < lw.count; ++t) {
+    const uint32_t entry = lw.entry(t);
+    if (t + 1 < lw.count) {
+      if (t + 1 - lw.base == kWave) lw.load(t + 1, lane);  // nothing else in flight here
+      issue(lw.entry(t + 1), (t + 1) & 1);
     }
-    __syncthreads();
+    const KvStageFwd& st = ring[t & 1];
     int ro_t = ro;
     TrOffsets tro_t = tro;
     opaque(ro_t);
     opaque(tro_t.lo);
     opaque(tro_t.hi);
-    if (entry & kFullBit) {
-      RowIntervals iv{};
-      fwd_tile<false>(s_k, s_v, qf, oacc, m_run, l_run, iv, a.scale_log2, ro_t, tro_t, g);
-    } else {
-      RowIntervals iv;
-      iv.at_tile(static_cast<int>(key0), cb, ce, db, de);
-      fwd_tile<true>(s_k, s_v, qf, oacc, m_run, l_run, iv, a.scale_log2, ro_t, tro_t, g);
-    }
+    RowIntervals iv;
+    iv.at_tile(static_cast<int>((entry & ~kFullBit) * kTN), cb, ce, db, de);
+    fwd_tile(st.k, st.v, qf, oacc, m_run, l_run, !(entry & kFullBit), iv, a.scale_log2, ro_t, tro_t, g);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's loads of tile t+1 have landed
+    lds_barrier();
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -379,43 +442,45 @@ __global__ void __launch_bounds__(256) attn_bwd_acc_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// dQ: query-major, same traversal as the forward. dQ^T = K^T dS^T. One LDS buffer (so two
-// workgroups share a CU) with the next tile prefetched into registers.
+// dQ: query-major, same traversal and K/V ring as the forward. dQ^T = K^T dS^T.
 // ---------------------------------------------------------------------------------------------
-template <bool PARTIAL>
 __device__ __forceinline__ void dq_tile(const uint16_t* sk, const uint16_t* sv,
                                         const bf16x8 (&qf)[8], const bf16x8 (&df)[8],
-                                        f32x16 (&dqacc)[4], float lse2, float delta,
+                                        f32x16 (&dqacc)[4], float lse2, float delta, bool partial,
                                         const RowIntervals& iv, float scale_log2, int ro,
                                         const TrOffsets& tro, int g) {
-  bf16x8 dsb[4];
   const RowOperand none{nullptr, 0};
+  const float neg_lse2 = -lse2;
+  // One 32-key half at a time: dS of the half goes straight into dQ (8 registers of dS live).
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
+    bf16x8 dsb[2];
     f32x16 s, dp;
     mfma_chains2(s, dp, RowOperand{sk + kb * 32 * kRowLd, ro}, RowOperand{sv + kb * 32 * kRowLd, ro},
                  qf, df, none, none);
+    if (partial) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = iv.visible(kb * 32 + c_row(r, g)) ? s[r] : -INFINITY;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      float p = fast_exp2(s[r] * scale_log2 - lse2);
-      if (PARTIAL) p = iv.visible(kb * 32 + c_row(r, g)) ? p : 0.f;
+      const float p = fast_exp2(fmaf(s[r], scale_log2, neg_lse2));
       s[r] = p * (dp[r] - delta);
     }
-    dsb[kb * 2 + 0] = pack_c_half(s, 0);
-    dsb[kb * 2 + 1] = pack_c_half(s, 8);
+    dsb[0] = pack_c_half(s, 0);
+    dsb[1] = pack_c_half(s, 8);
+    mfma_tr_blocks<2>(dqacc, sk + kb * 32 * kRowLd, tro, dsb);
   }
-  mfma_tr_blocks<4>(dqacc, sk, tro, dsb);
 }
 
 template <int G>
 __global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
-  constexpr int NT = kWave * G;
-  __shared__ __attribute__((aligned(16))) uint16_t s_k[kTN * kRowLd];
-  __shared__ __attribute__((aligned(16))) uint16_t s_v[kTN * kRowLd];
+  __shared__ __attribute__((aligned(16))) KvStageFwd ring[2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(wave >= 0 && wave < G);
   const int g = lane >> 5;
   const int c = lane & 31;
   const int hkv = blockIdx.x % a.hkv;
@@ -424,6 +489,18 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
   const int64_t qrow = m * kTM + c;
   const bool valid_q = qrow < a.nq;
   const int64_t qsafe = valid_q ? qrow : a.nq - 1;
+
+  const uint16_t* kbase = a.k + hkv * a.ksh;
+  const uint16_t* vbase = a.v + hkv * a.vsh;
+  const int nk = static_cast<int>(a.nk);
+  ListWindow lw{a.plan.f_list + m * a.plan.nnf, a.plan.f_cnt[m], 0, 0};
+  lw.load(0, lane);
+  const KvTileLanes lanes(lane);
+  auto issue = [&](uint32_t entry, int stage) {
+    const int key0 = static_cast<int>(entry & ~kFullBit) * kTN;
+    issue_kv_tile<G>(kbase, a.kst, vbase, a.vst, key0, nk, ring[stage], wave, lanes);
+  };
+  if (lw.count > 0) issue(lw.entry(0), 0);
 
   bf16x8 qf[8], df[8];
   load_row_frag(qf, a.q + qsafe * a.qst + head * a.qsh, valid_q, g);
@@ -438,36 +515,29 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
   }
 
   f32x16 dqacc[4] = {};
-  const uint16_t* kbase = a.k + hkv * a.ksh;
-  const uint16_t* vbase = a.v + hkv * a.vsh;
-  const int count = a.plan.f_cnt[m];
-  const int32_t* list = a.plan.f_list + m * a.plan.nnf;
   const int ro = row_operand_off(c, g);
   const TrOffsets tro(lane);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  lds_barrier();
 
-  for (int t = 0; t < count; ++t) {
-    const uint32_t entry = static_cast<uint32_t>(list[t]);
-    const int64_t key0 = static_cast<int64_t>(entry & ~kFullBit) * kTN;
-    const int valid = static_cast<int>(min<int64_t>(kTN, a.nk - key0));
-    __syncthreads();
-    {
-      TileLoader<NT, kTN> tile;
-      tile.load(kbase + key0 * a.kst, a.kst, valid, tid);
-      tile.store(s_k, tid);
-      tile.load(vbase + key0 * a.vst, a.vst, valid, tid);
-      tile.store(s_v, tid);
+  for (int t = 0; t < lw.count; ++t) {
+    const uint32_t entry = lw.entry(t);
+    if (t + 1 < lw.count) {
+      if (t + 1 - lw.base == kWave) lw.load(t + 1, lane);  // nothing else in flight here
+      issue(lw.entry(t + 1), (t + 1) & 1);
     }
-    __syncthreads();
+    const KvStageFwd& st = ring[t & 1];
     int ro_t = ro;
     TrOffsets tro_t = tro;
-    if (entry & kFullBit) {
-      RowIntervals iv{};
-      dq_tile<false>(s_k, s_v, qf, df, dqacc, lse2, delta, iv, a.scale_log2, ro_t, tro_t, g);
-    } else {
-      RowIntervals iv;
-      iv.at_tile(static_cast<int>(key0), cb, ce, db, de);
-      dq_tile<true>(s_k, s_v, qf, df, dqacc, lse2, delta, iv, a.scale_log2, ro_t, tro_t, g);
-    }
+    opaque(ro_t);
+    opaque(tro_t.lo);
+    opaque(tro_t.hi);
+    RowIntervals iv;
+    iv.at_tile(static_cast<int>((entry & ~kFullBit) * kTN), cb, ce, db, de);
+    dq_tile(st.k, st.v, qf, df, dqacc, lse2, delta, !(entry & kFullBit), iv, a.scale_log2, ro_t,
+            tro_t, g);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's loads of tile t+1 have landed
+    lds_barrier();
   }
   if (valid_q) store_row_c(a.dq + qrow * a.dqst + head * a.dqsh, dqacc, a.scale, g);
 }
@@ -502,30 +572,6 @@ struct KvStage {
 };
 static_assert(offsetof(KvStage, delta) == offsetof(KvStage, lse2) + 4 * kBwdTileM, "layout");
 static_assert(offsetof(KvStage, ends) == offsetof(KvStage, delta) + 4 * kBwdTileM, "layout");
-
-// Direct global -> LDS loads (gfx950 global_load_lds_dword / _dwordx4): lane l's bytes land at
-// `lds_wave_base` + l * size; the base, which goes through M0, must be the same for the whole
-// wave. They are issued from inline assembly so the compiler's wait-count bookkeeping never sees
-// them: it would otherwise wait for every one of them before each LDS read and barrier, which
-// defeats loading two iterations ahead. Callers wait for them explicitly (vmcnt). The compiler's
-// own vector loads are issued before or after these and return in order, so its waits stay
-// correct (at worst they also cover these loads). M0 is written one instruction before its use.
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-      (const __attribute__((address_space(3))) char*)(p))));
-}
-__device__ __forceinline__ void lds_load16(const void* src, void* lds_wave_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :
-               : "s"(lds_address(lds_wave_base)), "v"(src)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void lds_load4(const void* src, void* lds_wave_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
-               :
-               : "s"(lds_address(lds_wave_base)), "v"(src)
-               : "memory", "m0");
-}
 
 // P of one iteration in C-register order: [slice][register quad][lane].
 struct PExchange {
@@ -666,22 +712,6 @@ __device__ __forceinline__ void dkdv_store(const f32x16 (&acc)[4], float* t, int
   }
 }
 
-// s_waitcnt immediates: at most `n` vector-memory loads of this wave outstanding / all LDS
-// operations of this wave complete (the other counters left at their maxima).
-constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-constexpr int kLgkmcnt0 = 0xF | (0x3 << 14) | (0x7 << 4);
-
-// Workgroup barrier for LDS traffic this wave has already waited for. Unlike __syncthreads() it
-// does not wait for outstanding global -> LDS loads (the caller waits for the ones it needs with
-// vmcnt). The wavefront-scope fences emit nothing; they keep the compiler from moving memory
-// operations across the barrier.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) DkdvShared sh;
   KvStage& st0 = sh.walk.st[0];
@@ -820,6 +850,8 @@ int validate(const AttnArgs& a, int64_t head_dim) {
     return set_error(ASPEC_ERR_INVALID, "query heads must be divisible by the matching KV head count");
   if (a.group > kMaxGroup)
     return set_error(ASPEC_ERR_UNSUPPORTED, "GQA group %d exceeds %d", a.group, kMaxGroup);
+  if ((a.kst > 0 && a.kst >= (1LL << 30) / kBwdTileN) || (a.vst > 0 && a.vst >= (1LL << 30) / kBwdTileN))
+    return set_error(ASPEC_ERR_UNSUPPORTED, "K/V token stride too large for 32-bit tile offsets");
   if (a.nk >= (1LL << 31) - kBwdTileN)
     return set_error(ASPEC_ERR_INVALID, "too many keys for int32 tile indexing");
   return ASPEC_OK;

@@ -84,62 +84,136 @@ __device__ __forceinline__ void l1_terms(float p, float q, float& l1, float& pos
   else zero += p;
 }
 
+// log2-domain exponent of a logit against its row maximum: p = exp2(v*log2e - max*log2e) / sum.
+// The forward and backward kernels evaluate it with this one formula, so they classify p against
+// q identically, and identical draft/teacher rows give bitwise equal probabilities.
+__device__ __forceinline__ float neg_scaled_max(float m) { return -(m * kLog2e); }
+__device__ __forceinline__ float scaled_exp2(float v, float nm) { return fexp2(fmaf(v, kLog2e, nm)); }
+
+// (max, sum) pairs: sum is relative to max. A pair whose max is -inf holds 0 (all masked) or NaN
+// (a NaN logit) and passes through unscaled; +inf maxima give NaN, as softmax does.
+__device__ __forceinline__ void merge_max_sum(float& m, float& s, float mo, float so) {
+  const float mn = fmaxf(m, mo);
+  const float a = m == -INFINITY ? s : s * fexp2((m - mn) * kLog2e);
+  const float b = mo == -INFINITY ? so : so * fexp2((mo - mn) * kLog2e);
+  m = mn;
+  s = a + b;
+}
+
+// Block-wide merge of NP (max, sum) pairs; the result is broadcast to every thread.
+template <int NP>
+__device__ __forceinline__ void block_max_sum(float (&m)[NP], float (&s)[NP], float* scratch) {
+#pragma unroll
+  for (int i = 0; i < NP; ++i)
+    for (int off = 32; off > 0; off >>= 1)
+      merge_max_sum(m[i], s[i], __shfl_xor(m[i], off), __shfl_xor(s[i], off));
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      scratch[(2 * i) * 32 + wave] = m[i];
+      scratch[(2 * i + 1) * 32 + wave] = s[i];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    float mm = scratch[(2 * i) * 32], ss = scratch[(2 * i + 1) * 32];
+    for (int w = 1; w < nwaves; ++w) merge_max_sum(mm, ss, scratch[(2 * i) * 32 + w], scratch[(2 * i + 1) * 32 + w]);
+    // a row of -inf (or padding only) has no softmax: NaN, as torch gives
+    m[i] = mm;
+    s[i] = mm == -INFINITY ? NAN : ss;
+  }
+}
+
+__device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
+
+// Emits nothing; makes the packed chunks look modified, so each pass unpacks them afresh instead
+// of the compiler keeping 16 unpacked floats per chunk alive across passes (which spills).
 template <int NV>
-__global__ void __launch_bounds__(1024) loss_fwd_resident(LossArgs a) {
+__device__ __forceinline__ void opaque_chunks(uint4 (&v)[NV]) {
+#pragma unroll
+  for (int j = 0; j < NV; ++j) asm volatile("" : "+v"(v[j].x), "+v"(v[j].y), "+v"(v[j].z), "+v"(v[j].w));
+}
+__device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// This thread's (max, sum-exp) over the packed row chunks `v`.
+template <int NV>
+__device__ __forceinline__ void thread_max_sum(uint4 (&v)[NV], float& m, float& s) {
+  m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m = fmaxf(m, fmaxf(lo_bf(w[e]), hi_bf(w[e])));
+  }
+  opaque_chunks(v);
+  const float nm = m == -INFINITY ? 0.f : neg_scaled_max(m);
+  s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s += scaled_exp2(lo_bf(w[e]), nm) + scaled_exp2(hi_bf(w[e]), nm);
+    __builtin_amdgcn_sched_barrier(0);  // one chunk at a time: keeps the exps from piling up in registers
+  }
+}
+
+// Row-resident forward: 1024 threads hold one row of draft and teacher logits as packed bf16
+// (8*NV registers per tensor), read from HBM exactly once. At <= 64 VGPRs two rows share a CU, so
+// one row's loads overlap the other's arithmetic. Each thread reduces its own chunk to a
+// (max, sum-exp) pair; one block merge gives the row's softmax, a second pass the L1 terms.
+template <int NV>
+__global__ void __launch_bounds__(1024, 8) loss_fwd_resident(LossArgs a) {
   __shared__ float scratch[4 * 32];
   const int64_t row = blockIdx.x;
   const bool has_y = a.y != nullptr;
   const int64_t trow = has_y ? teacher_row(a, row) : 0;
   const uint16_t* xr = a.x + row * a.V;
   const uint16_t* yr = has_y && trow >= 0 ? a.y + trow * a.V : nullptr;
-  constexpr int E = NV * 8;
-  float xv[E], yv[E];
+  uint4 xs[NV], ys[NV];
+  const uint4* xq = reinterpret_cast<const uint4*>(xr);
+  const uint4* yq = reinterpret_cast<const uint4*>(yr);
+  const uint32_t nchunks = static_cast<uint32_t>(a.V / 8);
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int64_t col = (static_cast<int64_t>(j) * blockDim.x + threadIdx.x) * 8;
-    uint4 xs = make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u);  // -inf padding
-    uint4 ys = xs;
-    if (col < a.V) {
-      xs = *reinterpret_cast<const uint4*>(xr + col);
-      if (yr) ys = *reinterpret_cast<const uint4*>(yr + col);
-    }
-    const uint32_t xw[4] = {xs.x, xs.y, xs.z, xs.w};
-    const uint32_t yw[4] = {ys.x, ys.y, ys.z, ys.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xv[j * 8 + 2 * e] = __uint_as_float(xw[e] << 16);
-      xv[j * 8 + 2 * e + 1] = __uint_as_float(xw[e] & 0xffff0000u);
-      yv[j * 8 + 2 * e] = __uint_as_float(yw[e] << 16);
-      yv[j * 8 + 2 * e + 1] = __uint_as_float(yw[e] & 0xffff0000u);
+    const uint32_t chunk = j * 1024u + threadIdx.x;  // 32-bit offsets: one base register pair
+    xs[j] = make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u);  // -inf padding
+    ys[j] = xs[j];
+    if (chunk < nchunks) {
+      xs[j] = xq[chunk];
+      if (yr) ys[j] = yq[chunk];
     }
   }
-  float mx[2] = {-INFINITY, -INFINITY};
-#pragma unroll
-  for (int i = 0; i < E; ++i) {
-    mx[0] = fmaxf(mx[0], xv[i]);
-    mx[1] = fmaxf(mx[1], yv[i]);
-  }
-  block_reduce<2, true>(mx, scratch);
-  float sums[2] = {0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < E; ++i) {
-    xv[i] = fexp2((xv[i] - mx[0]) * kLog2e);
-    yv[i] = fexp2((yv[i] - mx[1]) * kLog2e);
-    sums[0] += xv[i];
-    sums[1] += yv[i];
-  }
-  block_reduce<2, false>(sums, scratch);
-  const float ix = 1.f / sums[0], iy = 1.f / sums[1];
+  float m[2], s[2];
+  thread_max_sum(xs, m[0], s[0]);
+  thread_max_sum(ys, m[1], s[1]);
+  opaque_chunks(xs);
+  opaque_chunks(ys);
+  block_max_sum<2>(m, s, scratch);
+  const float nmx = neg_scaled_max(m[0]), nmy = neg_scaled_max(m[1]);
+  const float ix = 1.f / s[0], iy = 1.f / s[1];
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   if (has_y) {
 #pragma unroll
-    for (int i = 0; i < E; ++i) l1_terms(xv[i] * ix, yv[i] * iy, acc[0], acc[1], acc[2], acc[3]);
+    for (int j = 0; j < NV; ++j) {
+      const uint32_t xw[4] = {xs[j].x, xs[j].y, xs[j].z, xs[j].w};
+      const uint32_t yw[4] = {ys[j].x, ys[j].y, ys[j].z, ys[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        l1_terms(scaled_exp2(lo_bf(xw[e]), nmx) * ix, scaled_exp2(lo_bf(yw[e]), nmy) * iy, acc[0], acc[1], acc[2], acc[3]);
+        l1_terms(scaled_exp2(hi_bf(xw[e]), nmx) * ix, scaled_exp2(hi_bf(yw[e]), nmy) * iy, acc[0], acc[1], acc[2], acc[3]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
     block_reduce<4, false>(acc, scratch);
   }
   if (threadIdx.x == 0) {
-    const float lse = logf(sums[0]) + mx[0];
+    const float lse = logf(s[0]) + m[0];
     float* st = a.stats + row * kStats;
-    st[0] = mx[0]; st[1] = ix; st[2] = mx[1]; st[3] = iy;
+    st[0] = m[0]; st[1] = ix; st[2] = m[1]; st[3] = iy;
     st[4] = acc[1]; st[5] = acc[2]; st[6] = acc[3]; st[7] = lse;
     if (a.l1) a.l1[row] = (has_y && trow >= 0) ? acc[0] : NAN;
     if (a.ce) {
@@ -162,32 +236,36 @@ __global__ void __launch_bounds__(256) loss_fwd_streaming(LossArgs a) {
   const int64_t trow = has_y ? teacher_row(a, row) : 0;
   const uint16_t* xr = a.x + row * a.V;
   const uint16_t* yr = has_y && trow >= 0 ? a.y + trow * a.V : nullptr;
-  float mx[2] = {-INFINITY, -INFINITY};
+  float m[2] = {-INFINITY, -INFINITY};
   for (int64_t i = threadIdx.x; i < a.V; i += blockDim.x) {
-    mx[0] = fmaxf(mx[0], bf(xr[i]));
-    if (yr) mx[1] = fmaxf(mx[1], bf(yr[i]));
+    m[0] = fmaxf(m[0], bf(xr[i]));
+    if (yr) m[1] = fmaxf(m[1], bf(yr[i]));
   }
-  block_reduce<2, true>(mx, scratch);
-  float sums[2] = {0.f, 0.f};
-  for (int64_t i = threadIdx.x; i < a.V; i += blockDim.x) {
-    sums[0] += fexp2((bf(xr[i]) - mx[0]) * kLog2e);
-    if (yr) sums[1] += fexp2((bf(yr[i]) - mx[1]) * kLog2e);
+  float s[2] = {0.f, 0.f};
+  {
+    const float nx = m[0] == -INFINITY ? 0.f : neg_scaled_max(m[0]);
+    const float ny = m[1] == -INFINITY ? 0.f : neg_scaled_max(m[1]);
+    for (int64_t i = threadIdx.x; i < a.V; i += blockDim.x) {
+      s[0] += scaled_exp2(bf(xr[i]), nx);
+      if (yr) s[1] += scaled_exp2(bf(yr[i]), ny);
+    }
   }
-  block_reduce<2, false>(sums, scratch);
-  const float ix = 1.f / sums[0], iy = 1.f / sums[1];
+  block_max_sum<2>(m, s, scratch);
+  const float nmx = neg_scaled_max(m[0]), nmy = neg_scaled_max(m[1]);
+  const float ix = 1.f / s[0], iy = 1.f / s[1];
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   if (has_y) {
     for (int64_t i = threadIdx.x; i < a.V; i += blockDim.x) {
-      const float p = fexp2((bf(xr[i]) - mx[0]) * kLog2e) * ix;
-      const float q = yr ? fexp2((bf(yr[i]) - mx[1]) * kLog2e) * iy : NAN;
+      const float p = scaled_exp2(bf(xr[i]), nmx) * ix;
+      const float q = yr ? scaled_exp2(bf(yr[i]), nmy) * iy : NAN;
       l1_terms(p, q, acc[0], acc[1], acc[2], acc[3]);
     }
     block_reduce<4, false>(acc, scratch);
   }
   if (threadIdx.x == 0) {
-    const float lse = logf(sums[0]) + mx[0];
+    const float lse = logf(s[0]) + m[0];
     float* st = a.stats + row * kStats;
-    st[0] = mx[0]; st[1] = ix; st[2] = mx[1]; st[3] = iy;
+    st[0] = m[0]; st[1] = ix; st[2] = m[1]; st[3] = iy;
     st[4] = acc[1]; st[5] = acc[2]; st[6] = acc[3]; st[7] = lse;
     if (a.l1) a.l1[row] = (has_y && trow >= 0) ? acc[0] : NAN;
     if (a.ce) {
@@ -205,10 +283,10 @@ __global__ void __launch_bounds__(256) loss_fwd_streaming(LossArgs a) {
 // dx = g_ce * (p - onehot(t)) + g_l1 * p * centered  (tiled_l1.py:107-127 for the L1 part).
 __device__ __forceinline__ float grad_elem(float x, float y, const float* st, float gl1, float gce,
                                            bool is_target, bool has_y) {
-  const float p = fexp2((x - st[0]) * kLog2e) * st[1];
+  const float p = scaled_exp2(x, neg_scaled_max(st[0])) * st[1];
   float d = 0.f;
   if (has_y) {
-    const float q = fexp2((y - st[2]) * kLog2e) * st[3];
+    const float q = scaled_exp2(y, neg_scaled_max(st[2])) * st[3];
     const float pos = st[4], neg = st[5], zero = st[6];
     const float centered = p > q ? 2.f * neg + zero : (p < q ? -2.f * pos - zero : neg - pos);
     d = p * centered * gl1;
