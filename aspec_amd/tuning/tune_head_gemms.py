@@ -1,0 +1,57 @@
+"""Writes the PyTorch TunableOp solution file for the selective-head GEMMs of the config-2 draft
+step on gfx950 (run on the GPU box; the file travels with the tree).
+
+The three products are plain library GEMMs (hipBLASLt / rocBLAS), bf16 in, fp32 accumulate:
+  draft logits   [8192, 4096] x W^T            (W = frozen head [32000, 4096])
+  teacher table  [4096, 4096] x W^T
+  head dgrad     [8192, 32000] x W             (computed on W^T stored contiguous: TN layout)
+TunableOp times every hipBLASLt and rocBLAS solution for each shape and records the fastest; with
+tuning off and this file loaded, later processes reuse the choice. The file carries validators
+(PyTorch, HIP, hipBLASLt, rocBLAS versions and the GPU arch); on a mismatch TunableOp ignores it
+and the library defaults run.
+
+    python -m aspec_amd.tuning.tune_head_gemms [--out PATH]
+"""
+
+from __future__ import annotations
+
+import argparse
+from pathlib import Path
+
+DEFAULT_FILE = Path(__file__).resolve().parent / "head_gemms_gfx950.csv"
+
+
+def main() -> None:
+    p = argparse.ArgumentParser()
+    p.add_argument("--out", default=str(DEFAULT_FILE))
+    p.add_argument("--rows", type=int, default=8192)
+    p.add_argument("--context", type=int, default=4096)
+    p.add_argument("--hidden", type=int, default=4096)
+    p.add_argument("--vocab", type=int, default=32000)
+    args = p.parse_args()
+    import torch
+
+    out = Path(args.out)
+    if out.exists():
+        out.unlink()
+    torch.cuda.tunable.enable(True)
+    torch.cuda.tunable.tuning_enable(True)
+    torch.cuda.tunable.set_filename(str(out))
+    torch.cuda.tunable.set_max_tuning_duration(300)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    h = torch.randn(args.rows, args.hidden, device=dev, dtype=torch.bfloat16, generator=g)
+    th = torch.randn(args.context, args.hidden, device=dev, dtype=torch.bfloat16, generator=g)
+    w = torch.randn(args.vocab, args.hidden, device=dev, dtype=torch.bfloat16, generator=g) * 0.02
+    wt = w.t().contiguous()
+    gr = torch.randn(args.rows, args.vocab, device=dev, dtype=torch.bfloat16, generator=g)
+    for _ in range(2):
+        torch.matmul(h, w.t())
+        torch.matmul(th, w.t())
+        torch.matmul(gr, wt.t())
+    torch.cuda.synchronize()
+    print(f"tuned head GEMMs -> {out} (written at exit)", flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -3,11 +3,13 @@
 One step = one packed 4096-token row through the draft hot path, inputs resident in HBM:
   1. THD row metadata + attention plan (HIP integer kernels),
   2. DSpark block-sparse attention forward (HIP, bf16 MFMA, GQA 32/8 x 128, 512 anchors x 16),
-  3. selective-head projection: draft logits = O[8192, 4096] @ W^T (W [32000, 4096], hipBLASLt) and
-     the frozen-teacher table = target_hidden[4096, 4096] @ W^T (no grad),
+  3. selective-head projection: draft logits = O[8192, 4096] @ W^T (W [32000, 4096], frozen) and
+     the frozen-teacher table = target_hidden[4096, 4096] @ W^T (no grad); library GEMMs
+     (hipBLASLt / rocBLAS) with the solutions recorded in aspec_amd/tuning/head_gemms_gfx950.csv,
   4. fused CE + softmax-L1 (HIP, indexed teacher rows), objective (0.1 CE + 0.9 L1) weighted by the
      DSpark eval mask x exp(-k/4) decay, normalised by the weight sum,
-  5. backward: dlogits (HIP), dO = dlogits @ W (hipBLASLt), attention backward (HIP);
+  5. backward: dlogits (HIP), dO = dlogits @ W (on the frozen head's transposed copy), attention
+     backward (HIP);
   before the head: injected-anchor validation, output-block counts and the DSpark targets (labels,
   eval mask, decay weights) from the anchors (HIP).
 Row-level operations that run once per row outside the step (packing collator, document anchor
@@ -45,6 +47,8 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the timed CPU oracle leg")
     p.add_argument("--no-kernel-timing", action="store_true", help="no per-kernel HIP events")
+    p.add_argument("--no-gemm-tuning", action="store_true",
+                   help="library-default GEMM solutions instead of the recorded TunableOp file")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (5 times): the reference kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -83,6 +87,9 @@ def build_inputs(device, seed):
         "head": randn(VOCAB, HIDDEN, scale=0.02),
         "target_hidden": randn(w.context_length, HIDDEN),
     }
+    # the head is frozen (dspark.py:359-368): its transposed copy is made once, so the dgrad GEMM
+    # runs in the TN layout the libraries serve fastest
+    x["head_t"] = x["head"].t().contiguous()
     x["input_ids"] = torch.randint(0, VOCAB, (1, w.context_length), generator=g).to(device)
     x["loss_mask"] = torch.ones(1, w.context_length, dtype=torch.long, device=device)
     t = lambda a, dt: torch.as_tensor(a, dtype=dt, device=device)[None]  # noqa: E731
@@ -102,18 +109,18 @@ class _Head:
 
         class HeadProjection(torch.autograd.Function):
             @staticmethod
-            def forward(ctx, hidden, weight):
+            def forward(ctx, hidden, weight, weight_t):
                 with _timing.region("head_gemm_fwd"):
                     out = torch.matmul(hidden, weight.t())
-                ctx.save_for_backward(weight)
+                ctx.save_for_backward(weight_t)
                 return out
 
             @staticmethod
             def backward(ctx, grad):
-                (weight,) = ctx.saved_tensors
+                (weight_t,) = ctx.saved_tensors
                 with _timing.region("head_gemm_dgrad"):
-                    dh = torch.matmul(grad, weight)
-                return dh, None
+                    dh = torch.matmul(grad, weight_t.t())
+                return dh, None, None
 
         return HeadProjection
 
@@ -151,7 +158,7 @@ def step(x, head_fn):
         x[name].grad = None
     out, _ = direct_cp_attention_from_kv(x["q"], x["k"], x["v"], meta)
     hidden = out.transpose(1, 2).reshape(w.num_queries, w.q_heads * w.head_dim)
-    logits = head_fn.apply(hidden, x["head"])
+    logits = head_fn.apply(hidden, x["head"], x["head_t"])
     ce, l1 = ce_l1_from_logits(logits, targets.target_ids.reshape(-1), teacher,
                                teacher_indices=targets.teacher_index.reshape(-1))
     wts = targets.weights.reshape(-1)
@@ -239,6 +246,25 @@ def aux_rows(device, w, reps):
     return {k: (stats[k]["mean_ms"], stats[k]["launches"], work[k]) for k in work if k in stats}
 
 
+def use_gemm_solutions():
+    """Points PyTorch's TunableOp at the recorded head-GEMM solutions (tuning off), through a temporary
+    copy so that nothing is written into the tree. Must run before torch is imported."""
+    import shutil
+    import tempfile
+    from pathlib import Path
+
+    src = Path(__file__).resolve().parent / "aspec_amd" / "tuning" / "head_gemms_gfx950.csv"
+    if not src.exists():
+        return None
+    tmp = Path(tempfile.mkdtemp(prefix="aspec_tunableop_"))
+    # TunableOp reads <name><device ordinal>.csv for the file name it is given
+    shutil.copyfile(src, tmp / "head_gemms0.csv")
+    os.environ["PYTORCH_TUNABLEOP_ENABLED"] = "1"
+    os.environ["PYTORCH_TUNABLEOP_TUNING"] = "0"
+    os.environ["PYTORCH_TUNABLEOP_FILENAME"] = str(tmp / "head_gemms.csv")
+    return str(src.relative_to(Path(__file__).resolve().parent))
+
+
 def measured_traffic(region):
     """HBM bytes per launch (read + write) of a region's kernel, from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
@@ -320,6 +346,7 @@ def main():
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
+    gemm_solutions = None if args.no_gemm_tuning else use_gemm_solutions()
     import torch
 
     from aspec_amd import _lib, _timing
@@ -402,6 +429,8 @@ def main():
                         "(CE + tiled L1, indexed teacher)",
             "context_tokens": w.context_length, "draft_queries": w.num_queries,
             "parallelism": "single GPU, CP=1",
+            "head_gemms": (f"library GEMMs, TunableOp solutions from {gemm_solutions}" if gemm_solutions
+                           else "library GEMMs, default solutions"),
         },
         "roofline": roofline,
         "attention": attn,
