@@ -712,6 +712,7 @@ __device__ __forceinline__ void dkdv_store(const f32x16 (&acc)[4], float* t, int
   }
 }
 
+template <int G>
 __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) DkdvShared sh;
   KvStage& st0 = sh.walk.st[0];
@@ -737,7 +738,7 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   const int count = __builtin_amdgcn_readfirstlane(a.plan.b_cnt[n]);
   const int first = chunk * kBwdChunk;
   const int last = min(count, first + kBwdChunk);
-  const int iters = max(0, last - first) * a.group;
+  const int iters = max(0, last - first) * G;
   const int32_t* list = a.plan.b_list + n * a.plan.nmb;
   const int64_t key0 = n * kBwdTileN;
   // The unit's (at most 32) query tiles, one per lane, read with readlane in the loop: no memory
@@ -762,8 +763,8 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   const int lcol = ((lane & 15) ^ swz(lrow)) * 8;
   const bool three_loads = wave < 3;
   auto row_base = [&](int it, int64_t& q0, int& head, int& valid) {
-    q0 = static_cast<int64_t>(__builtin_amdgcn_readlane(my_tile, it / a.group)) * kBwdTileM;
-    head = hkv * a.group + it % a.group;
+    q0 = static_cast<int64_t>(__builtin_amdgcn_readlane(my_tile, it / G)) * kBwdTileM;
+    head = hkv * G + it % G;
     valid = static_cast<int>(min<int64_t>(kBwdTileM, a.nq - q0));
   };
   auto issue = [&](int it, KvStage& sb) {
@@ -983,8 +984,17 @@ extern "C" int aspec_dspark_attn_bwd_stages(
     if ((rc = check_launch("attn_bwd_dq_kernel"))) return rc;
   }
   if (stages & 4) {
-    hipLaunchKernelGGL(attn_bwd_dkdv_kernel, dim3(static_cast<uint32_t>(a.plan.max_units * a.hkv)),
-                       dim3(kWave * kDkdvWaves), 0, s, a);
+    const dim3 grid(static_cast<uint32_t>(a.plan.max_units * a.hkv)), block(kWave * kDkdvWaves);
+    switch (a.group) {  // the group size is a compile-time constant inside the walk
+      case 1: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<1>, grid, block, 0, s, a); break;
+      case 2: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<2>, grid, block, 0, s, a); break;
+      case 3: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<3>, grid, block, 0, s, a); break;
+      case 4: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<4>, grid, block, 0, s, a); break;
+      case 5: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<5>, grid, block, 0, s, a); break;
+      case 6: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<6>, grid, block, 0, s, a); break;
+      case 7: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<7>, grid, block, 0, s, a); break;
+      default: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<8>, grid, block, 0, s, a); break;
+    }
     if ((rc = check_launch("attn_bwd_dkdv_kernel"))) return rc;
   }
   if (stages & 8) {
