@@ -181,23 +181,6 @@ __device__ __forceinline__ void lds_load4(const void* src, void* lds_wave_base) 
 }
 
 
-// s_waitcnt immediates: at most `n` vector-memory loads of this wave outstanding / all LDS
-// operations of this wave complete (the other counters left at their maxima).
-constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-constexpr int kLgkmcnt0 = 0xF | (0x3 << 14) | (0x7 << 4);
-
-// Workgroup barrier for LDS traffic this wave has already waited for. Unlike __syncthreads() it
-// does not wait for outstanding global -> LDS loads (the caller waits for the ones it needs with
-// vmcnt). The wavefront-scope fences emit nothing; they keep the compiler from moving memory
-// operations across the barrier.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-
 // K/V tile ring of the query-major kernels (forward, dQ): two stages, each a 64-key K tile and V
 // tile in swizzled rows, filled straight from global memory (no staging registers). Stage t+1 is
 // loading while stage t is computed; one wait and one barrier per tile.

@@ -47,6 +47,22 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // exp2 as the bare v_exp_f32 (inputs here are <= 8 or -inf; no range fix-up needed).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// s_waitcnt immediates: at most `n` vector-memory loads of this wave outstanding / all LDS
+// operations of this wave complete (the other counters left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+constexpr int kLgkmcnt0 = 0xF | (0x3 << 14) | (0x7 << 4);
+
+// Workgroup barrier for LDS traffic this wave has already waited for. Unlike __syncthreads() it
+// does not wait for outstanding global -> LDS loads (the caller waits for the ones it needs with
+// vmcnt). The wavefront-scope fences emit nothing; they keep the compiler from moving memory
+// operations across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
   return v;

@@ -1,10 +1,12 @@
 // Vocabulary-sliced loss kernels: softmax-L1 (tiled_l1.py semantics) and cross-entropy, forward
 // and backward, alone or fused. HBM-bound streaming reductions.
 //
-// Forward, one workgroup per row:
-//   resident path (V % 8 == 0, V <= 1024*8*4): 1024 threads read the draft row and the teacher row
-//   from HBM exactly once into registers, then reduce max / sum / |p - q| / sign masses;
-//   streaming path (any V): 256 threads, element loads, the rows re-read from cache per pass.
+// Forward:
+//   row walk (V % 8 == 0, V <= 512*8*8): one 512-thread workgroup per CU walks the rows; each row
+//   of draft and teacher logits is read from HBM exactly once into registers while the previous
+//   row is reduced (max / sum / |p - q| / sign masses);
+//   streaming path (any V): one 256-thread workgroup per row, element loads, the rows re-read
+//   from cache per pass.
 // Backward: elementwise over rows x V from the saved per-row statistics (one read of x and y,
 // one write of dx).
 //
@@ -129,102 +131,193 @@ __device__ __forceinline__ void block_max_sum(float (&m)[NP], float (&s)[NP], fl
 }
 
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
-
-// Emits nothing; makes the packed chunks look modified, so each pass unpacks them afresh instead
-// of the compiler keeping 16 unpacked floats per chunk alive across passes (which spills).
-template <int NV>
-__device__ __forceinline__ void opaque_chunks(uint4 (&v)[NV]) {
-#pragma unroll
-  for (int j = 0; j < NV; ++j) asm volatile("" : "+v"(v[j].x), "+v"(v[j].y), "+v"(v[j].z), "+v"(v[j].w));
-}
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// This thread's (max, sum-exp) over the packed row chunks `v`.
+constexpr int kWalkThreads = 512;  // threads of the persistent row walk (8 waves, 2 per SIMD)
+constexpr int kWalkWaves = kWalkThreads / 64;
+
 template <int NV>
-__device__ __forceinline__ void thread_max_sum(uint4 (&v)[NV], float& m, float& s) {
+__device__ __forceinline__ void chunk_exps(const uint4 (&v)[NV], float (&e)[NV * 8], float& m,
+                                           float& sum) {
   m = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) m = fmaxf(m, fmaxf(lo_bf(w[e]), hi_bf(w[e])));
+    for (int k = 0; k < 4; ++k) m = fmaxf(m, fmaxf(lo_bf(w[k]), hi_bf(w[k])));
   }
-  opaque_chunks(v);
   const float nm = m == -INFINITY ? 0.f : neg_scaled_max(m);
-  s = 0.f;
+  sum = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s += scaled_exp2(lo_bf(w[e]), nm) + scaled_exp2(hi_bf(w[e]), nm);
-    __builtin_amdgcn_sched_barrier(0);  // one chunk at a time: keeps the exps from piling up in registers
+    for (int k = 0; k < 4; ++k) {
+      e[j * 8 + 2 * k] = scaled_exp2(lo_bf(w[k]), nm);
+      e[j * 8 + 2 * k + 1] = scaled_exp2(hi_bf(w[k]), nm);
+      sum += e[j * 8 + 2 * k] + e[j * 8 + 2 * k + 1];
+    }
   }
 }
 
-// Row-resident forward: 1024 threads hold one row of draft and teacher logits as packed bf16
-// (8*NV registers per tensor), read from HBM exactly once. At <= 64 VGPRs two rows share a CU, so
-// one row's loads overlap the other's arithmetic. Each thread reduces its own chunk to a
-// (max, sum-exp) pair; one block merge gives the row's softmax, a second pass the L1 terms.
-template <int NV>
-__global__ void __launch_bounds__(1024, 8) loss_fwd_resident(LossArgs a) {
-  __shared__ float scratch[4 * 32];
-  const int64_t row = blockIdx.x;
-  const bool has_y = a.y != nullptr;
-  const int64_t trow = has_y ? teacher_row(a, row) : 0;
-  const uint16_t* xr = a.x + row * a.V;
-  const uint16_t* yr = has_y && trow >= 0 ? a.y + trow * a.V : nullptr;
-  uint4 xs[NV], ys[NV];
-  const uint4* xq = reinterpret_cast<const uint4*>(xr);
-  const uint4* yq = reinterpret_cast<const uint4*>(yr);
-  const uint32_t nchunks = static_cast<uint32_t>(a.V / 8);
+// Merges every thread's (max, sum) pair for NP quantities; `slots` holds 2*NP*kWalkWaves floats.
+template <int NP>
+__device__ __forceinline__ void block_merge(float (&m)[NP], float (&sm)[NP], float* slots) {
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const uint32_t chunk = j * 1024u + threadIdx.x;  // 32-bit offsets: one base register pair
-    xs[j] = make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u);  // -inf padding
-    ys[j] = xs[j];
-    if (chunk < nchunks) {
-      xs[j] = xq[chunk];
-      if (yr) ys[j] = yq[chunk];
+  for (int i = 0; i < NP; ++i)
+    for (int off = 32; off > 0; off >>= 1)
+      merge_max_sum(m[i], sm[i], __shfl_xor(m[i], off), __shfl_xor(sm[i], off));
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      slots[(2 * i) * kWalkWaves + wave] = m[i];
+      slots[(2 * i + 1) * kWalkWaves + wave] = sm[i];
     }
   }
-  float m[2], s[2];
-  thread_max_sum(xs, m[0], s[0]);
-  thread_max_sum(ys, m[1], s[1]);
-  opaque_chunks(xs);
-  opaque_chunks(ys);
-  block_max_sum<2>(m, s, scratch);
-  const float nmx = neg_scaled_max(m[0]), nmy = neg_scaled_max(m[1]);
-  const float ix = 1.f / s[0], iy = 1.f / s[1];
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  if (has_y) {
+  lds_barrier();
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    float mm = slots[(2 * i) * kWalkWaves], ss = slots[(2 * i + 1) * kWalkWaves];
+#pragma unroll
+    for (int w = 1; w < kWalkWaves; ++w)
+      merge_max_sum(mm, ss, slots[(2 * i) * kWalkWaves + w], slots[(2 * i + 1) * kWalkWaves + w]);
+    m[i] = mm;
+    sm[i] = mm == -INFINITY ? NAN : ss;  // a row of -inf (or padding only): NaN, as torch gives
+  }
+}
+
+template <int NP>
+__device__ __forceinline__ void block_sums(float (&v)[NP], float* slots) {
+#pragma unroll
+  for (int i = 0; i < NP; ++i)
+    for (int off = 32; off > 0; off >>= 1) v[i] += __shfl_xor(v[i], off);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) slots[i * kWalkWaves + wave] = v[i];
+  }
+  lds_barrier();
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    float r = slots[i * kWalkWaves];
+#pragma unroll
+    for (int w = 1; w < kWalkWaves; ++w) r += slots[i * kWalkWaves + w];
+    v[i] = r;
+  }
+}
+
+template <int NV>
+__global__ void __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+loss_fwd_persistent(LossArgs args) {
+  __shared__ float merge_slots[4 * kWalkWaves];  // (max, sum) of x and y per wave
+  __shared__ float sum_slots[4 * kWalkWaves];    // |p-q|, p>q, p<q masses and sum p per wave
+  // Every field in a local: referencing the kernel argument itself from the loop would make the
+  // compiler copy it to scratch.
+  const uint16_t* const xbase = args.x;
+  const uint16_t* const ybase = args.y;
+  const int64_t* const yidx = args.yidx;
+  const int64_t trows = args.trows;
+  const int64_t* const target = args.target;
+  const int64_t ignore = args.ignore_index;
+  const int64_t rows = args.rows, V = args.V;
+  float* const l1_out = args.l1;
+  float* const ce_out = args.ce;
+  float* const stats = args.stats;
+  int32_t* const flags = args.flags;
+  const int tid = threadIdx.x;
+  const bool has_y = ybase != nullptr;
+  const uint32_t nchunks = static_cast<uint32_t>(V / 8);
+  const uint4 ninf = make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u);  // -inf
+  uint4 nx[NV], ny[NV];
+  auto fetch = [&](int64_t r, int64_t tr) {
+    const uint4* xq = reinterpret_cast<const uint4*>(xbase + r * V);
+    const uint4* yq = has_y && tr >= 0 ? reinterpret_cast<const uint4*>(ybase + tr * V) : nullptr;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      const uint32_t xw[4] = {xs[j].x, xs[j].y, xs[j].z, xs[j].w};
-      const uint32_t yw[4] = {ys[j].x, ys[j].y, ys[j].z, ys[j].w};
+      const uint32_t chunk = j * static_cast<uint32_t>(kWalkThreads) + tid;
+      nx[j] = ninf;
+      ny[j] = ninf;
+      if (chunk < nchunks) {
+        nx[j] = xq[chunk];
+        if (yq) ny[j] = yq[chunk];
+      }
+    }
+  };
+  auto teacher = [&](int64_t r) -> int64_t {  // teacher row of draft row r, -1 when out of range
+    if (!has_y) return 0;
+    if (!yidx) return r;
+    const int64_t t = yidx[r];
+    if (t < 0 || t >= trows) {
+      atomicOr(flags, 1);
+      return -1;
+    }
+    return t;
+  };
+  int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  int64_t trow = teacher(row);
+  int64_t tgt = ce_out ? target[row] : ignore;
+  fetch(row, trow);
+  while (row < rows) {
+    // the next row's index and target, loaded while this row is computed
+    const int64_t next = row + gridDim.x;
+    int64_t trow_n = 0, tgt_n = ignore;
+    if (next < rows) {
+      trow_n = teacher(next);
+      tgt_n = ce_out ? target[next] : ignore;
+    }
+    // the CE target logit (thread 0, from L2: the row has just been read)
+    const bool tgt_ok = tgt != ignore && tgt >= 0 && tgt < V;
+    float target_logit = 0.f;
+    if (tid == 0 && tgt_ok) target_logit = bf(xbase[row * V + tgt]);
+    float ex[NV * 8], ey[NV * 8];
+    float m[2], sm[2];
+    chunk_exps(nx, ex, m[0], sm[0]);
+    m[1] = -INFINITY;
+    sm[1] = 0.f;
+    if (has_y) chunk_exps(ny, ey, m[1], sm[1]);
+    // The target logit and the next row's index have arrived before the next row's loads go out,
+    // so no later wait for them also waits for those loads. The loads stay below the last read of
+    // this row's packed registers, which they reuse.
+    asm volatile("" ::"v"(target_logit), "v"(trow_n), "v"(tgt_n));
+    __builtin_amdgcn_sched_barrier(0);
+    if (next < rows) fetch(next, trow_n);
+    const float mx_local = m[0], my_local = m[1];
+    block_merge<2>(m, sm, merge_slots);
+    // p = e * 2^((m_local - M) log2e) / S per thread (0 for threads whose chunk is all -inf)
+    const float cx = (mx_local == -INFINITY ? 0.f : fexp2((mx_local - m[0]) * kLog2e)) / sm[0];
+    const float cy = (my_local == -INFINITY ? 0.f : fexp2((my_local - m[1]) * kLog2e)) / sm[1];
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // |p-q|, mass p>q, mass p<q, sum p
+    if (has_y) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        l1_terms(scaled_exp2(lo_bf(xw[e]), nmx) * ix, scaled_exp2(lo_bf(yw[e]), nmy) * iy, acc[0], acc[1], acc[2], acc[3]);
-        l1_terms(scaled_exp2(hi_bf(xw[e]), nmx) * ix, scaled_exp2(hi_bf(yw[e]), nmy) * iy, acc[0], acc[1], acc[2], acc[3]);
+      for (int i = 0; i < NV * 8; ++i) {
+        const float pv = ex[i] * cx, qv = ey[i] * cy;
+        acc[0] += fabsf(pv - qv);
+        acc[1] += pv > qv ? pv : 0.f;
+        acc[2] += pv < qv ? pv : 0.f;
+        acc[3] += pv;
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
-    block_reduce<4, false>(acc, scratch);
-  }
-  if (threadIdx.x == 0) {
-    const float lse = logf(s[0]) + m[0];
-    float* st = a.stats + row * kStats;
-    st[0] = m[0]; st[1] = ix; st[2] = m[1]; st[3] = iy;
-    st[4] = acc[1]; st[5] = acc[2]; st[6] = acc[3]; st[7] = lse;
-    if (a.l1) a.l1[row] = (has_y && trow >= 0) ? acc[0] : NAN;
-    if (a.ce) {
-      const int64_t t = a.target[row];
-      float v = 0.f;
-      if (t != a.ignore_index) {
-        if (t < 0 || t >= a.V) { atomicOr(a.flags, 2); v = NAN; }
-        else v = lse - bf(xr[t]);
+    block_sums<4>(acc, sum_slots);
+    if (tid == 0) {
+      const float lse = logf(sm[0]) + m[0];
+      float* st = stats + row * kStats;
+      st[0] = m[0]; st[1] = 1.f / sm[0]; st[2] = m[1]; st[3] = 1.f / sm[1];
+      st[4] = acc[1]; st[5] = acc[2]; st[6] = acc[3] - acc[1] - acc[2]; st[7] = lse;
+      if (l1_out) l1_out[row] = (has_y && trow >= 0) ? acc[0] : NAN;
+      if (ce_out) {
+        float v = 0.f;
+        if (tgt != ignore) {
+          if (!tgt_ok) { atomicOr(flags, 2); v = NAN; }
+          else v = lse - target_logit;
+        }
+        ce_out[row] = v;
       }
-      a.ce[row] = v;
     }
+    row = next;
+    trow = trow_n;
+    tgt = tgt_n;
   }
 }
 
@@ -348,12 +441,18 @@ int launch_fwd(const LossArgs& a, hipStream_t s) {
   const bool vec = a.V % 8 == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
                    (!a.y || (reinterpret_cast<uintptr_t>(a.y) & 15) == 0);
   const dim3 grid(static_cast<uint32_t>(a.rows));
-  if (vec && a.V <= 1024 * 8 * 1) {
-    hipLaunchKernelGGL(loss_fwd_resident<1>, grid, dim3(1024), 0, s, a);
-  } else if (vec && a.V <= 1024 * 8 * 2) {
-    hipLaunchKernelGGL(loss_fwd_resident<2>, grid, dim3(1024), 0, s, a);
-  } else if (vec && a.V <= 1024 * 8 * 4) {
-    hipLaunchKernelGGL(loss_fwd_resident<4>, grid, dim3(1024), 0, s, a);
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return set_error(ASPEC_ERR_RUNTIME, "cannot query the GPU's compute-unit count");
+  const dim3 walk(static_cast<uint32_t>(std::min<int64_t>(a.rows, cus)));
+  const dim3 block(kWalkThreads);
+  if (vec && a.V <= kWalkThreads * 8 * 2) {
+    hipLaunchKernelGGL(loss_fwd_persistent<2>, walk, block, 0, s, a);
+  } else if (vec && a.V <= kWalkThreads * 8 * 4) {
+    hipLaunchKernelGGL(loss_fwd_persistent<4>, walk, block, 0, s, a);
+  } else if (vec && a.V <= kWalkThreads * 8 * 8) {
+    hipLaunchKernelGGL(loss_fwd_persistent<8>, walk, block, 0, s, a);
   } else {
     hipLaunchKernelGGL(loss_fwd_streaming, grid, dim3(256), 0, s, a);
   }

@@ -199,7 +199,7 @@ def kernel_work(w):
 # kernel names as the committed rocprofv3 summaries list them (namespace and arguments dropped)
 _REGION_KERNEL = {"attn_fwd": "attn_fwd_kernel<4>", "attn_bwd_dq": "attn_bwd_dq_kernel<4>",
                   "attn_bwd_dkdv": "attn_bwd_dkdv_kernel", "attn_bwd_prepare": "attn_bwd_pre_kernel",
-                  "loss_fwd": "loss_fwd_resident<4>", "loss_bwd": "loss_bwd_kernel<true>"}
+                  "loss_fwd": "loss_fwd_persistent<8>", "loss_bwd": "loss_bwd_kernel<true>"}
 
 
 def aux_rows(device, w, reps):
