@@ -1,7 +1,8 @@
 """aspec_amd: MI355X-native (gfx950 HIP) DSpark draft hot path.
 
 Drop-in replacements for the reference operators of aspec/models/ops (direct CP / THD attention,
-THD sparse metadata, tiled L1, the selective-head losses), the packing collator
+THD sparse metadata, tiled L1, the selective-head losses, the fused Q/K RMSNorm + RoPE), the
+packing collator
 (aspec/data/utils.py), the anchor layout (anchors.py), output-block compaction (output_blocks.py)
 and the DSpark targets (dspark.py), backed by hand-written HIP kernels in libaspec_amd.so,
 reached through the C ABI of include/aspec_amd.h.
@@ -22,6 +23,10 @@ from aspec_amd.direct_cp import (  # noqa: F401
     direct_cp_attention_from_kv,
     direct_cp_attention_observation,
 )
+from aspec_amd.dspark_qk_norm_rope import (  # noqa: F401
+    dspark_qk_norm_rope,
+    dspark_qk_norm_rope_available,
+)
 from aspec_amd.targets import decay_weights, dspark_targets  # noqa: F401
 from aspec_amd.output_blocks import (  # noqa: F401
     output_block_counts,
@@ -39,6 +44,8 @@ __all__ = [
     "DFlashPackingCollator",
     "decay_weights",
     "document_anchor_slots",
+    "dspark_qk_norm_rope",
+    "dspark_qk_norm_rope_available",
     "dspark_targets",
     "output_block_counts",
     "output_block_indices",

@@ -318,6 +318,49 @@ int aspec_dspark_targets(const int64_t* anchors, const uint8_t* keep, const int6
                          int64_t* target_ids, int64_t* prev_ids, int64_t* teacher_index,
                          float* eval_mask, float* weights, void* stream);
 
+/*
+ * DSpark Q/K preparation, forward: per-head RMSNorm of query and keys, the context/draft key join
+ * and indexed RoPE. Replaces `dspark_qk_norm_rope` / `_DSparkQkNormRope.forward`
+ * (aspec/models/ops/dspark_qk_norm_rope.py:134-280, run_dspark_qk_norm_rope); the math is
+ * `_prepare_dflash_qk` (aspec/models/draft/dflash.py:280-327) in fp32 with one rounding to bf16.
+ *
+ * bf16, head_dim 128: query [batch*draft_len][q_heads][128], context_key [batch*context_len]
+ * [kv_heads][128], draft_key [batch*draft_len][kv_heads][128]; q_weight, k_weight [128];
+ * cos, sin [rope_rows][rope_stride] (first 128 columns used); positions int64, one per token.
+ * Outputs: q_out like query; k_out [batch][context_len + draft_len][kv_heads][128] (context first);
+ * rstd_q [batch*draft_len][q_heads], rstd_k [batch*(context_len+draft_len)][kv_heads] fp32.
+ * A position outside [0, rope_rows) gives a NaN output row and sets bit 0 of *status_flags.
+ */
+int aspec_qk_norm_rope_fwd(const void* query, const void* context_key, const void* draft_key,
+                           const void* q_weight, const void* k_weight, const void* cos,
+                           const void* sin, int64_t rope_rows, int64_t rope_stride,
+                           const int64_t* query_positions, const int64_t* context_positions,
+                           const int64_t* draft_positions, int64_t batch, int64_t context_len,
+                           int64_t draft_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                           float eps, void* q_out, void* k_out, float* rstd_q, float* rstd_k,
+                           int32_t* status_flags, void* stream);
+
+/* Bytes of the backward's workspace (per-workgroup weight-gradient partials). */
+int aspec_qk_norm_rope_bwd_workspace_bytes(int64_t batch, int64_t context_len, int64_t draft_len,
+                                           int64_t q_heads, int64_t kv_heads, size_t* bytes);
+
+/*
+ * DSpark Q/K preparation, backward (`_DSparkQkNormRope.backward`,
+ * aspec/models/ops/dspark_qk_norm_rope.py:282-398, run_dspark_qk_norm_rope_bwd): grad_q / grad_k
+ * in the forward's output layouts -> d_query, d_context_key, d_draft_key (bf16, input layouts) and
+ * dw_q, dw_k (fp32 [128], deterministic). rstd_q / rstd_k are the forward's.
+ */
+int aspec_qk_norm_rope_bwd(const void* grad_q, const void* grad_k, const void* query,
+                           const void* context_key, const void* draft_key, const float* rstd_q,
+                           const float* rstd_k, const void* q_weight, const void* k_weight,
+                           const void* cos, const void* sin, int64_t rope_rows,
+                           int64_t rope_stride, const int64_t* query_positions,
+                           const int64_t* context_positions, const int64_t* draft_positions,
+                           int64_t batch, int64_t context_len, int64_t draft_len, int64_t q_heads,
+                           int64_t kv_heads, int64_t head_dim, float eps, void* d_query,
+                           void* d_context_key, void* d_draft_key, float* dw_q, float* dw_k,
+                           void* workspace, int32_t* status_flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,4 +15,9 @@ How each part is pinned (besides agreeing with the HIP path):
                   single-visible-key closed forms and autograd-vs-finite-difference gradients.
   loss.py      -- fp64 closed forms pinned by special values (identical rows -> 0, disjoint
                   one-hots -> 2, uniform CE -> log V) and finite-difference gradients.
+  rows.py      -- the reference's own packing / anchor / output-block / target test cases and
+                  closed forms.
+  qk_norm_rope.py -- RMSNorm and RoPE closed forms: constant rows normalize to +-1, cos=1/sin=0
+                  is the identity, cos=0/sin=1 is rotate_half, the rotation keeps each (i, i+D/2)
+                  pair's norm, and finite-difference gradients.
 """
