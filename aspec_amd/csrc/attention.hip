@@ -542,6 +542,11 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
 // (global_load_lds_dwordx4: no staging registers), so every load has two iterations to arrive.
 // One barrier per iteration.
 // ---------------------------------------------------------------------------------------------
+template <bool P>
+struct Role {
+  static constexpr bool value = P;
+};
+
 constexpr int kDkdvWaves = 2 * kKvWaves;
 constexpr int kDkdvStages = 4;
 
@@ -771,14 +776,27 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
     else if (three_loads) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3));
     else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2));
   };
+  // The edge trips (dS waves at trip 0, P waves at trip iters) run their step like every other
+  // trip, on zeros: stage 3 and P buffer 1 start zeroed, and the P waves' extra step sees no
+  // visible row. Their contributions are exact zeros, and no accumulator is merged across a
+  // branch inside the walk.
+  {
+    constexpr int n3 = static_cast<int>(sizeof(KvStage) / 16), np = static_cast<int>(sizeof(PExchange) / 16);
+    static_assert(sizeof(KvStage) % 16 == 0 && sizeof(PExchange) % 16 == 0, "16-byte fills");
+    uint4* z3 = reinterpret_cast<uint4*>(&st3);
+    uint4* zp = reinterpret_cast<uint4*>(&px1);
+    for (int i = tid; i < n3; i += kWave * kDkdvWaves) z3[i] = make_uint4(0, 0, 0, 0);
+    for (int i = tid; i < np; i += kWave * kDkdvWaves) zp[i] = make_uint4(0, 0, 0, 0);
+  }
   if (iters > 0) issue(0, st0);
   if (iters > 1) issue(1, st1);
   wait_loads(iters > 1);
   lds_barrier();
 
   // Trip i (stage ring position K = i % 4): P waves on stage i, dS waves on stage i-1, loads of
-  // iteration i+2 into stage i+2.
-  auto trip = [&](auto kc, int i, KvStage& s_cur, KvStage& s_prv, KvStage& s_ld, PExchange& x_cur,
+  // iteration i+2 into stage i+2. Each role runs its own copy of the walk (same trips, same
+  // barriers).
+  auto trip = [&](auto role, int i, KvStage& s_cur, KvStage& s_prv, KvStage& s_ld, PExchange& x_cur,
                   PExchange& x_prv) {
     const bool ahead = i + 2 < iters;
     if (ahead) issue(i + 2, s_ld);
@@ -787,30 +805,34 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
     opaque(ro_t);
     opaque(tro_t.lo);
     opaque(tro_t.hi);
-    if (p_role) {
-      if (i < iters) {
-        int64_t q0;
-        int head, valid;
-        row_base(i, q0, head, valid);
-        dkdv_p_step(s_cur, x_cur, kvf, acc, a.scale_log2, w, valid,
-                    static_cast<int>(key0) + w * 32, ro_t, tro_t, lane);
-      }
-    } else if (i > 0) {
-      dkdv_ds_step(s_prv, x_prv, kvf, acc, w, ro_t, tro_t, lane);
+    if constexpr (decltype(role)::value) {
+      const bool live = i < iters;
+      int64_t q0;
+      int head, valid;
+      row_base(i, q0, head, valid);
+      dkdv_p_step(live ? s_cur : st3, x_cur, kvf, acc, a.scale_log2, w, live ? valid : 0,
+                  static_cast<int>(key0) + w * 32, ro_t, tro_t, lane);
+    } else {
+      dkdv_ds_step(s_prv, x_prv, kvf, acc, w, ro_t, tro_t, lane);  // trip 0: stage 3 and buffer 1
     }
     wait_loads(ahead);  // this wave's part of stage i+1 has landed
     lds_barrier();
-    (void)kc;
   };
-  for (int i = 0; i <= iters; i += 4) {
-    trip(0, i, st0, st3, st2, px0, px1);
-    if (i + 1 > iters) break;
-    trip(1, i + 1, st1, st0, st3, px1, px0);
-    if (i + 2 > iters) break;
-    trip(2, i + 2, st2, st1, st0, px0, px1);
-    if (i + 3 > iters) break;
-    trip(3, i + 3, st3, st2, st1, px1, px0);
-  }
+  auto walk = [&](auto role) {
+    for (int i = 0; i <= iters; i += 4) {
+      trip(role, i, st0, st3, st2, px0, px1);
+      if (i + 1 > iters) break;
+      trip(role, i + 1, st1, st0, st3, px1, px0);
+      if (i + 2 > iters) break;
+      trip(role, i + 2, st2, st1, st0, px0, px1);
+      if (i + 3 > iters) break;
+      trip(role, i + 3, st3, st2, st1, px1, px0);
+    }
+  };
+  if (p_role)
+    walk(Role<true>{});
+  else
+    walk(Role<false>{});
   // Epilogue in the walk's LDS (every load has landed): P waves (dV) first, then dS waves (dK).
   const bool direct = a.plan.b_chunks[n] == 1;
   const int64_t ws_stride = static_cast<int64_t>(a.hkv) * kHeadDim;
