@@ -1,8 +1,8 @@
 """aspec_amd: MI355X-native (gfx950 HIP) DSpark draft hot path.
 
 Drop-in replacements for the reference operators of aspec/models/ops (direct CP / THD attention,
-THD sparse metadata, tiled L1, the selective-head losses, the fused Q/K RMSNorm + RoPE), the
-packing collator
+THD sparse metadata, tiled L1, the selective-head losses, the fused Q/K RMSNorm + RoPE, the DSpark
+head terms with the Markov bias and confidence head), the packing collator
 (aspec/data/utils.py), the anchor layout (anchors.py), output-block compaction (output_blocks.py)
 and the DSpark targets (dspark.py), backed by hand-written HIP kernels in libaspec_amd.so,
 reached through the C ABI of include/aspec_amd.h.
@@ -23,6 +23,14 @@ from aspec_amd.direct_cp import (  # noqa: F401
     direct_cp_attention_from_kv,
     direct_cp_attention_observation,
 )
+from aspec_amd.dspark_head import (  # noqa: F401
+    AcceptRatePredictor,
+    VanillaMarkov,
+    acceptance_statistics,
+    build_markov_head,
+    dspark_prediction_terms,
+    markov_head_logits,
+)
 from aspec_amd.dspark_qk_norm_rope import (  # noqa: F401
     dspark_qk_norm_rope,
     dspark_qk_norm_rope_available,
@@ -41,7 +49,13 @@ from aspec_amd.thd_sparse_metadata import build_thd_sparse_pair  # noqa: F401
 from aspec_amd.tiled_l1 import tiled_l1_from_logits  # noqa: F401
 
 __all__ = [
+    "AcceptRatePredictor",
     "DFlashPackingCollator",
+    "VanillaMarkov",
+    "acceptance_statistics",
+    "build_markov_head",
+    "dspark_prediction_terms",
+    "markov_head_logits",
     "decay_weights",
     "document_anchor_slots",
     "dspark_qk_norm_rope",

@@ -55,6 +55,9 @@ SIGNATURES = {
     "aspec_ce_l1_fwd": (
         _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64] + [_c_void_p] * 5
     ),
+    "aspec_ce_l1_argmax_fwd": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64] + [_c_void_p] * 6
+    ),
     "aspec_ce_l1_bwd": (
         _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64] + [_c_void_p] * 5
     ),
@@ -86,7 +89,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib = None

@@ -33,6 +33,7 @@ struct LossArgs {
   float* ce;
   float* stats;
   int32_t* flags;
+  int64_t* amax;  // row argmax (torch.argmax semantics), optional
   const float* g_l1;
   const float* g_ce;
   uint16_t* dx;
@@ -136,6 +137,8 @@ __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 
 constexpr int kWalkThreads = 512;  // threads of the persistent row walk (8 waves, 2 per SIMD)
 constexpr int kWalkWaves = kWalkThreads / 64;
 
+// Per-thread max and exp2 values of NV chunks of eight bf16 logits (chunk j of thread t holds
+// row elements (j * kWalkThreads + t) * 8 .. +7; value i of `e` is element i % 8 of chunk i / 8).
 template <int NV>
 __device__ __forceinline__ void chunk_exps(const uint4 (&v)[NV], float (&e)[NV * 8], float& m,
                                            float& sum) {
@@ -187,15 +190,27 @@ __device__ __forceinline__ void block_merge(float (&m)[NP], float (&sm)[NP], flo
   }
 }
 
+// Row argmax as torch.argmax defines it: the first NaN if the row has one (NaN compares above
+// everything), else the first index holding the maximum M. Keys order the candidates: NaN at
+// index i -> i, maximum at i -> i | 2^31, neither -> kNoKey; the row's argmax is the minimum key.
+constexpr uint32_t kNoKey = 0xffffffffu;
+__device__ __forceinline__ uint32_t argmax_key(float x, float M, uint32_t idx) {
+  return x != x ? idx : (x == M ? (idx | 0x80000000u) : kNoKey);
+}
+
+// Block sums of NP floats and the block minimum of one key (same barrier).
 template <int NP>
-__device__ __forceinline__ void block_sums(float (&v)[NP], float* slots) {
+__device__ __forceinline__ void block_sums(float (&v)[NP], uint32_t& key, float* slots,
+                                           uint32_t* key_slots) {
 #pragma unroll
   for (int i = 0; i < NP; ++i)
     for (int off = 32; off > 0; off >>= 1) v[i] += __shfl_xor(v[i], off);
+  for (int off = 32; off > 0; off >>= 1) key = min(key, static_cast<uint32_t>(__shfl_xor(static_cast<int>(key), off)));
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
 #pragma unroll
     for (int i = 0; i < NP; ++i) slots[i * kWalkWaves + wave] = v[i];
+    key_slots[wave] = key;
   }
   lds_barrier();
 #pragma unroll
@@ -205,13 +220,17 @@ __device__ __forceinline__ void block_sums(float (&v)[NP], float* slots) {
     for (int w = 1; w < kWalkWaves; ++w) r += slots[i * kWalkWaves + w];
     v[i] = r;
   }
+  key = key_slots[0];
+#pragma unroll
+  for (int w = 1; w < kWalkWaves; ++w) key = min(key, key_slots[w]);
 }
 
-template <int NV>
+template <int NV, bool ARGMAX>
 __global__ void __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 loss_fwd_persistent(LossArgs args) {
   __shared__ float merge_slots[4 * kWalkWaves];  // (max, sum) of x and y per wave
   __shared__ float sum_slots[4 * kWalkWaves];    // |p-q|, p>q, p<q masses and sum p per wave
+  __shared__ uint32_t key_slots[kWalkWaves];      // argmax key per wave
   // Every field in a local: referencing the kernel argument itself from the loop would make the
   // compiler copy it to scratch.
   const uint16_t* const xbase = args.x;
@@ -225,6 +244,7 @@ loss_fwd_persistent(LossArgs args) {
   float* const ce_out = args.ce;
   float* const stats = args.stats;
   int32_t* const flags = args.flags;
+  int64_t* const amax_out = args.amax;
   const int tid = threadIdx.x;
   const bool has_y = ybase != nullptr;
   const uint32_t nchunks = static_cast<uint32_t>(V / 8);
@@ -273,7 +293,7 @@ loss_fwd_persistent(LossArgs args) {
     if (tid == 0 && tgt_ok) target_logit = bf(xbase[row * V + tgt]);
     float ex[NV * 8], ey[NV * 8];
     float m[2], sm[2];
-    chunk_exps(nx, ex, m[0], sm[0]);
+    chunk_exps<NV>(nx, ex, m[0], sm[0]);
     m[1] = -INFINITY;
     sm[1] = 0.f;
     if (has_y) chunk_exps(ny, ey, m[1], sm[1]);
@@ -285,6 +305,28 @@ loss_fwd_persistent(LossArgs args) {
     if (next < rows) fetch(next, trow_n);
     const float mx_local = m[0], my_local = m[1];
     block_merge<2>(m, sm, merge_slots);
+    uint32_t key = kNoKey;
+    if (ARGMAX) {
+      const float M = m[0];
+      if (fabsf(M) >= 0x1p-14f && M < INFINITY && sm[0] == sm[0]) {
+        // A finite row without NaN whose maximum is not tiny: a thread holding M finds its first
+        // maximal element among its exp values, which hold exp2(x log2e - M log2e) (chunk_exps).
+        // The maximum gives exactly `emax` (same expression), and any other bf16 logit differs
+        // from M by at least |M| 2^-8, far above the rounding of M log2e, so it never does.
+        if (mx_local == M) {
+          const float emax = scaled_exp2(M, neg_scaled_max(M));
+          uint32_t i0 = 0;  // first exp value equal to emax (immediates: nothing hoisted per value)
+#pragma unroll
+          for (int i = NV * 8 - 1; i >= 0; --i) i0 = ex[i] == emax ? static_cast<uint32_t>(i) : i0;
+          key = ((((i0 >> 3) * kWalkThreads + tid) << 3) + (i0 & 7)) | 0x80000000u;
+        }
+      } else {
+        // a NaN, an infinity, an all -inf row or a tiny maximum: rescan the (cache-resident) row
+        const uint16_t* xr = xbase + row * V;
+        for (int64_t i = tid; i < V; i += kWalkThreads)
+          key = min(key, argmax_key(bf(xr[i]), M, static_cast<uint32_t>(i)));
+      }
+    }
     // p = e * 2^((m_local - M) log2e) / S per thread (0 for threads whose chunk is all -inf)
     const float cx = (mx_local == -INFINITY ? 0.f : fexp2((mx_local - m[0]) * kLog2e)) / sm[0];
     const float cy = (my_local == -INFINITY ? 0.f : fexp2((my_local - m[1]) * kLog2e)) / sm[1];
@@ -299,8 +341,9 @@ loss_fwd_persistent(LossArgs args) {
         acc[3] += pv;
       }
     }
-    block_sums<4>(acc, sum_slots);
+    block_sums<4>(acc, key, sum_slots, key_slots);
     if (tid == 0) {
+      if (ARGMAX) amax_out[row] = static_cast<int64_t>(key & 0x7fffffffu);
       const float lse = logf(sm[0]) + m[0];
       float* st = stats + row * kStats;
       st[0] = m[0]; st[1] = 1.f / sm[0]; st[2] = m[1]; st[3] = 1.f / sm[1];
@@ -344,6 +387,20 @@ __global__ void __launch_bounds__(256) loss_fwd_streaming(LossArgs a) {
     }
   }
   block_max_sum<2>(m, s, scratch);
+  if (a.amax) {  // first NaN, else first maximum (torch.argmax)
+    uint32_t key = kNoKey;
+    for (int64_t i = threadIdx.x; i < a.V; i += blockDim.x)
+      key = min(key, argmax_key(bf(xr[i]), m[0], static_cast<uint32_t>(i)));
+    for (int off = 32; off > 0; off >>= 1)
+      key = min(key, static_cast<uint32_t>(__shfl_xor(static_cast<int>(key), off)));
+    __shared__ uint32_t keys[8];
+    if ((threadIdx.x & 63) == 0) keys[threadIdx.x >> 6] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) key = min(key, keys[w]);
+      a.amax[row] = static_cast<int64_t>(key & 0x7fffffffu);
+    }
+  }
   const float nmx = neg_scaled_max(m[0]), nmy = neg_scaled_max(m[1]);
   const float ix = 1.f / s[0], iy = 1.f / s[1];
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -448,11 +505,14 @@ int launch_fwd(const LossArgs& a, hipStream_t s) {
   const dim3 walk(static_cast<uint32_t>(std::min<int64_t>(a.rows, cus)));
   const dim3 block(kWalkThreads);
   if (vec && a.V <= kWalkThreads * 8 * 2) {
-    hipLaunchKernelGGL(loss_fwd_persistent<2>, walk, block, 0, s, a);
+    if (a.amax) hipLaunchKernelGGL((loss_fwd_persistent<2, true>), walk, block, 0, s, a);
+    else hipLaunchKernelGGL((loss_fwd_persistent<2, false>), walk, block, 0, s, a);
   } else if (vec && a.V <= kWalkThreads * 8 * 4) {
-    hipLaunchKernelGGL(loss_fwd_persistent<4>, walk, block, 0, s, a);
+    if (a.amax) hipLaunchKernelGGL((loss_fwd_persistent<4, true>), walk, block, 0, s, a);
+    else hipLaunchKernelGGL((loss_fwd_persistent<4, false>), walk, block, 0, s, a);
   } else if (vec && a.V <= kWalkThreads * 8 * 8) {
-    hipLaunchKernelGGL(loss_fwd_persistent<8>, walk, block, 0, s, a);
+    if (a.amax) hipLaunchKernelGGL((loss_fwd_persistent<8, true>), walk, block, 0, s, a);
+    else hipLaunchKernelGGL((loss_fwd_persistent<8, false>), walk, block, 0, s, a);
   } else {
     hipLaunchKernelGGL(loss_fwd_streaming, grid, dim3(256), 0, s, a);
   }
@@ -486,10 +546,11 @@ using namespace aspec;
 
 extern "C" int aspec_loss_stats_floats(void) { return kStats; }
 
-extern "C" int aspec_ce_l1_fwd(const void* logits, const void* teacher, const int64_t* teacher_index,
-                               int64_t teacher_rows, const int64_t* targets, int64_t ignore_index,
-                               int64_t rows, int64_t vocab, float* l1_out, float* ce_out,
-                               float* stats, int32_t* status_flags, void* stream) {
+extern "C" int aspec_ce_l1_argmax_fwd(const void* logits, const void* teacher,
+                                      const int64_t* teacher_index, int64_t teacher_rows,
+                                      const int64_t* targets, int64_t ignore_index, int64_t rows,
+                                      int64_t vocab, float* l1_out, float* ce_out, int64_t* argmax_out,
+                                      float* stats, int32_t* status_flags, void* stream) {
   int rc = check_common(rows, vocab, logits);
   if (rc) return rc;
   if (!stats || !status_flags) return set_error(ASPEC_ERR_INVALID, "stats and status buffers are required");
@@ -509,7 +570,18 @@ extern "C" int aspec_ce_l1_fwd(const void* logits, const void* teacher, const in
   a.ce = ce_out;
   a.stats = stats;
   a.flags = status_flags;
+  a.amax = argmax_out;
+  if (argmax_out && vocab > 0x7fffffffLL)
+    return set_error(ASPEC_ERR_UNSUPPORTED, "argmax needs a vocabulary below 2^31");
   return launch_fwd(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int aspec_ce_l1_fwd(const void* logits, const void* teacher, const int64_t* teacher_index,
+                               int64_t teacher_rows, const int64_t* targets, int64_t ignore_index,
+                               int64_t rows, int64_t vocab, float* l1_out, float* ce_out,
+                               float* stats, int32_t* status_flags, void* stream) {
+  return aspec_ce_l1_argmax_fwd(logits, teacher, teacher_index, teacher_rows, targets, ignore_index,
+                                rows, vocab, l1_out, ce_out, nullptr, stats, status_flags, stream);
 }
 
 extern "C" int aspec_ce_l1_bwd(const void* logits, const void* teacher, const int64_t* teacher_index,

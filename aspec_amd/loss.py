@@ -30,7 +30,7 @@ def _check_logits(logits):
 
 class _CeL1(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, logits, targets, teacher, indices, ignore_index):
+    def forward(ctx, logits, targets, teacher, indices, ignore_index, want_argmax=False):
         vocab = logits.shape[-1]
         rows = logits.numel() // vocab
         dev = logits.device
@@ -39,22 +39,26 @@ class _CeL1(torch.autograd.Function):
         l1 = torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev) if teacher is not None else None
         flags = torch.zeros(1, dtype=torch.int32, device=dev)
         trows = teacher.shape[0] if (teacher is not None and indices is not None) else rows
+        amax = torch.empty(logits.shape[:-1], dtype=torch.int64, device=dev) if want_argmax else None
         with _timing.region("loss_fwd"):
-            _lib.call("aspec_ce_l1_fwd", _lib.ptr(logits), _lib.ptr(teacher), _lib.ptr(indices), trows,
-                      _lib.ptr(targets), ignore_index, rows, vocab, _lib.ptr(l1), _lib.ptr(ce),
-                      _lib.ptr(stats), _lib.ptr(flags), _lib.stream_handle(dev))
+            _lib.call("aspec_ce_l1_argmax_fwd", _lib.ptr(logits), _lib.ptr(teacher), _lib.ptr(indices),
+                      trows, _lib.ptr(targets), ignore_index, rows, vocab, _lib.ptr(l1), _lib.ptr(ce),
+                      _lib.ptr(amax), _lib.ptr(stats), _lib.ptr(flags), _lib.stream_handle(dev))
         ctx.save_for_backward(logits, targets, teacher, indices, stats)
         ctx.ignore_index = ignore_index
         ctx.trows = trows
         ctx.flags = flags
         ctx.set_materialize_grads(False)
         if l1 is None:
-            return ce, torch.zeros_like(ce)
-        return ce, l1
+            l1 = torch.zeros_like(ce)
+        if amax is None:
+            return ce, l1
+        ctx.mark_non_differentiable(amax)
+        return ce, l1, amax
 
     @staticmethod
     @once_differentiable
-    def backward(ctx, grad_ce, grad_l1):
+    def backward(ctx, grad_ce, grad_l1, grad_argmax=None):
         logits, targets, teacher, indices, stats = ctx.saved_tensors
         vocab = logits.shape[-1]
         rows = logits.numel() // vocab
@@ -62,17 +66,20 @@ class _CeL1(torch.autograd.Function):
         gl1 = None if (grad_l1 is None or teacher is None) else grad_l1.to(torch.float32).contiguous()
         grad_logits = torch.empty_like(logits)
         if gce is None and gl1 is None:
-            return grad_logits.zero_(), None, None, None, None
+            return grad_logits.zero_(), None, None, None, None, None
         with _timing.region("loss_bwd"):
             _lib.call("aspec_ce_l1_bwd", _lib.ptr(logits), _lib.ptr(teacher), _lib.ptr(indices),
                       ctx.trows, _lib.ptr(targets), ctx.ignore_index, rows, vocab, _lib.ptr(stats),
                       _lib.ptr(gl1), _lib.ptr(gce), _lib.ptr(grad_logits),
                       _lib.stream_handle(logits.device))
-        return grad_logits, None, None, None, None
+        return grad_logits, None, None, None, None, None
 
 
-def ce_l1_from_logits(logits, targets, teacher=None, *, teacher_indices=None, ignore_index=-100):
-    """Per-row (cross-entropy, softmax-L1) from bf16 logits in one pass (HIP)."""
+def ce_l1_from_logits(logits, targets, teacher=None, *, teacher_indices=None, ignore_index=-100,
+                      return_argmax=False):
+    """Per-row (cross-entropy, softmax-L1) from bf16 logits in one pass (HIP). With
+    `return_argmax`, also the row argmax (torch.argmax semantics: the first NaN, else the first
+    maximum) from the same pass, for the head's accuracy metric (dspark.py:625)."""
     _check_logits(logits)
     rows = logits.numel() // logits.shape[-1]
     if targets.dtype != torch.int64 or targets.numel() != rows or targets.device != logits.device:
@@ -93,7 +100,7 @@ def ce_l1_from_logits(logits, targets, teacher=None, *, teacher_indices=None, ig
                              "int64 index per Draft row")
         if teacher_indices is not None:
             teacher_indices = teacher_indices.reshape(-1).contiguous()
-    return _CeL1.apply(logits, targets, teacher, teacher_indices, ignore_index)
+    return _CeL1.apply(logits, targets, teacher, teacher_indices, ignore_index, return_argmax)
 
 
 def cross_entropy(logits, targets, ignore_index=-100):

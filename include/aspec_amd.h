@@ -189,6 +189,18 @@ int aspec_ce_l1_fwd(const void* logits, const void* teacher, const int64_t* teac
                     int32_t* status_flags, void* stream);
 
 /*
+ * aspec_ce_l1_fwd plus the row argmax in the same pass over the logits: argmax_out[r] (int64, may
+ * be NULL) is the index torch.argmax returns -- the first NaN if the row has one, else the first
+ * index of the row maximum. Vocabularies of 2^31 or more are rejected when argmax_out is set.
+ * Replaces, in the same pass, `logits.argmax(-1)` of the DSpark head's accuracy metric
+ * (aspec/models/dspark.py:628-629).
+ */
+int aspec_ce_l1_argmax_fwd(const void* logits, const void* teacher, const int64_t* teacher_index,
+                           int64_t teacher_rows, const int64_t* targets, int64_t ignore_index,
+                           int64_t rows, int64_t vocab, float* l1_out, float* ce_out,
+                           int64_t* argmax_out, float* stats, int32_t* status_flags, void* stream);
+
+/*
  * Fused backward: grad_logits = grad_ce[r] * (softmax(x_r) - onehot(targets[r]))
  *                             + grad_l1[r] * p * (sign(p - q) - E_p[sign(p - q)])
  * (the L1 term in the cancellation-free form of aspec/models/ops/tiled_l1.py:107-127).
