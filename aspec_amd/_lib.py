@@ -83,13 +83,23 @@ SIGNATURES = {
         _int, [_c_void_p] * 11 + [_i64, _i64] + [_c_void_p] * 3 + [_i64] * 6 + [_f32]
         + [_c_void_p] * 8
     ),
+    "aspec_rmsnorm_fwd": (_int, [_c_void_p] * 3 + [_i64, _i64, _f32] + [_c_void_p] * 4),
+    "aspec_rmsnorm_bwd_workspace_bytes": (_int, [_i64, _c_void_p]),
+    "aspec_rmsnorm_bwd": (_int, [_c_void_p] * 5 + [_i64, _i64] + [_c_void_p] * 4),
+    "aspec_swiglu_fwd": (_int, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
+    "aspec_swiglu_bwd": (_int, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p]),
+    "aspec_adamw_state_bytes": (_int, []),
+    "aspec_adamw_workspace_bytes": (_int, [_c_void_p]),
+    "aspec_adamw_step": (
+        _int, [_c_void_p] * 5 + [_i64] + [_f32] * 6 + [_c_void_p] * 3
+    ),
     "aspec_dspark_targets": (
         _int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p] + [_i64] * 5
         + [_c_void_p] * 8
     ),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib = None

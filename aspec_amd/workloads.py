@@ -10,6 +10,8 @@ All layouts are deterministic given the seed; nothing here reads data from disk.
   config 3: 64 log-normal documents (median 600, sigma 1, clipped to [32, 8192]) first-fit packed
             into 32768-token bins (one bin per workload), an anchor every 32 tokens, B = 16.
   config 4: one 32768-token document, 2048 anchors at linspace(0, 32768 - 16, 2048), GQA 40/8.
+  config 5: 3 documents of seeded lengths (sum 4096), an anchor every 8 doc-local tokens
+            (u <= L - B - 1), B = 16, GQA 32/8 x 128: the full one-layer training step's row.
 """
 
 from __future__ import annotations
@@ -117,6 +119,18 @@ def config4(seed: int = 0) -> Workload:
     T, N, B = 32768, 2048, 16
     anchors = np.round(np.linspace(0, T - B, N)).astype(np.int64)
     return from_layout("config4", [T], anchors, np.zeros(N, np.int64), B, q_heads=40, kv_heads=8)
+
+
+def config5(seed: int = 0) -> Workload:
+    rng = np.random.default_rng(seed)
+    cuts = np.sort(rng.choice(np.arange(512, 4096 - 512), size=2, replace=False))
+    lengths = np.diff(np.concatenate([[0], cuts, [4096]]))
+    # u <= L - B - 1: every block's last target stays in its document, as injected anchors must
+    # (anchors.py:107-116)
+    anchors, docs = _strided_anchors([n - 1 for n in lengths], 8, 16)
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]])
+    anchors = anchors - np.concatenate([[0], np.cumsum(np.asarray(lengths) - 1)[:-1]])[docs] + starts[docs]
+    return from_layout("config5", lengths, anchors, docs, 16)
 
 
 def reference_test_layout(block_size: int, lengths=(257, 263, 19), drop_doc: bool = True) -> Workload:

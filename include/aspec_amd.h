@@ -373,6 +373,60 @@ int aspec_qk_norm_rope_bwd(const void* grad_q, const void* grad_k, const void* q
                            void* d_context_key, void* d_draft_key, float* dw_q, float* dw_k,
                            void* workspace, int32_t* status_flags, void* stream);
 
+/*
+ * RMSNorm forward over rows of `hidden` bf16 values (multiple of 8, at most 8192), with an
+ * optional residual add: y = x + residual (bf16, written to y_out), rstd[r] = 1/sqrt(mean(y^2) +
+ * eps), out = bf16(y * rstd * weight). Replaces `DFlashRMSNorm.forward` / `_dflash_rms_norm`
+ * (aspec/models/draft/dflash.py:175-188, 282-293) and, with a residual, the residual add before
+ * `post_attention_layernorm` (dflash.py:1046-1050). residual and y_out may be NULL together.
+ */
+int aspec_rmsnorm_fwd(const void* x, const void* residual, const void* weight, int64_t rows,
+                      int64_t hidden, float eps, void* y_out, void* out, float* rstd, void* stream);
+
+/* Bytes of the RMSNorm backward's workspace (per-workgroup weight-gradient partials). */
+int aspec_rmsnorm_bwd_workspace_bytes(int64_t hidden, size_t* bytes);
+
+/*
+ * RMSNorm backward: with g = grad_out * weight and n = y * rstd,
+ * dy = rstd * (g - n * mean(g * n)) + dy_extra (bf16; dy_extra may be NULL) and
+ * dweight = sum over rows of grad_out * n (fp32 [hidden], deterministic). y and rstd are the
+ * forward's normalized input and rstd. Backward of `aspec_rmsnorm_fwd` (autograd of
+ * dflash.py:282-293).
+ */
+int aspec_rmsnorm_bwd(const void* grad_out, const void* dy_extra, const void* y, const void* weight,
+                      const float* rstd, int64_t rows, int64_t hidden, void* dy, float* dweight,
+                      void* workspace, void* stream);
+
+/*
+ * SwiGLU over one GEMM output gate_up = [gate | up] (rows x 2*ffn bf16, ffn a multiple of 8):
+ * out = bf16(silu(gate) * up). Replaces `act_fn(gate_proj(x)) * up_proj(x)` of `DFlashMLP`
+ * (aspec/models/draft/dflash.py:967-980).
+ */
+int aspec_swiglu_fwd(const void* gate_up, int64_t rows, int64_t ffn, void* out, void* stream);
+
+/* SwiGLU backward: d_gate_up = [dout * up * silu'(gate) | dout * silu(gate)] (bf16). */
+int aspec_swiglu_bwd(const void* grad_out, const void* gate_up, int64_t rows, int64_t ffn,
+                     void* d_gate_up, void* stream);
+
+/* Bytes of the device-side AdamW state (step count, clip coefficient, skip flag, ...); the caller
+ * zero-initializes it once. */
+int aspec_adamw_state_bytes(void);
+
+/* Bytes of the AdamW step's workspace (gradient-norm partials). */
+int aspec_adamw_workspace_bytes(size_t* bytes);
+
+/*
+ * One optimizer step of `BF16Optimizer` (aspec/training/optimizer.py:40-164: fp32 master weights,
+ * global-norm clipping to max_grad_norm, a non-finite norm skips the step, torch's fused AdamW,
+ * bf16 copy-back) over n flat parameters: params bf16, master / exp_avg / exp_avg_sq fp32, grads
+ * bf16 (all 16-byte aligned). The step count, clip coefficient and gradient norm stay in `state` on
+ * the device (no host synchronization).
+ */
+int aspec_adamw_step(void* params, float* master, float* exp_avg, float* exp_avg_sq,
+                     const void* grads, int64_t n, float lr, float weight_decay, float beta1,
+                     float beta2, float eps, float max_grad_norm, void* state, void* workspace,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,185 @@
+"""The one-layer DSpark training step on the GPU: RMSNorm (with the fused residual add), SwiGLU and
+the fused AdamW against the fp64 oracle (bf16 tolerances stated per test), the composed layer
+and its parameter gradients against the fp64 layer oracle at a reduced geometry, and three full
+steps at the Qwen3-8B geometry (config 5)."""
+
+import numpy as np
+import pytest
+import torch
+
+from aspec_amd import workloads as W
+from aspec_amd.draft_layer import (DSparkDraftLayerModel, FusedBF16Optimizer, dspark_layer_step,
+                                   layer_batch, rms_norm, swiglu, warmup_decay_lr)
+from oracle import layer as ol
+from oracle import loss as oloss
+from oracle import metadata as M
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().double().cpu().numpy()
+
+
+def _close(name, got, want, rel_l2, atol_frac):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    err = np.abs(got - want).max()
+    rel = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    print(f"{name}: max_abs={err:.3e} rel_l2={rel:.3e}")
+    assert rel < rel_l2, name
+    assert err <= atol_frac * max(np.abs(want).max(), 1e-30), name
+
+
+@pytest.mark.parametrize("hidden,residual", [(4096, False), (4096, True), (1000, True), (8192, False)])
+def test_rmsnorm_matches_oracle(gpu, hidden, residual):
+    g = torch.Generator(device=gpu).manual_seed(hidden)
+    rows = 96
+    x = (torch.randn(rows, hidden, device=gpu, generator=g) * 2).to(torch.bfloat16).requires_grad_()
+    r = (torch.randn(rows, hidden, device=gpu, generator=g)).to(torch.bfloat16).requires_grad_() if residual else None
+    w = (1 + 0.1 * torch.randn(hidden, device=gpu, generator=g)).to(torch.bfloat16).requires_grad_()
+    out = rms_norm(x, w, 1e-6, residual=r)
+    y, n = out if residual else (x, out)
+    dn = torch.randn(rows, hidden, device=gpu, generator=g).to(torch.bfloat16)
+    dy = torch.randn(rows, hidden, device=gpu, generator=g).to(torch.bfloat16) if residual else None
+    outs, grads = ((y, n), (dy, dn)) if residual else ((n,), (dn,))
+    torch.autograd.backward(outs, grads)
+    ry, rn = ol.rms_norm(_np(x), _np(w), 1e-6, residual=None if r is None else _np(r))
+    if residual:
+        # y is bf16(x + r): compare exactly against the rounded oracle sum
+        np.testing.assert_array_equal(_np(y), _np(torch.as_tensor(ry).to(torch.bfloat16)))
+        ry = _np(y)
+    _close("rmsnorm out", _np(n), ol.rms_norm(ry, _np(w), 1e-6)[1], 1e-2, 1e-2)
+    gdy, gdw = ol.rms_norm_grad(ry, _np(w), 1e-6, _np(dn), None if dy is None else _np(dy))
+    _close("rmsnorm dx", _np(x.grad), gdy, 1e-2, 2e-2)
+    if residual:
+        np.testing.assert_array_equal(_np(r.grad), _np(x.grad))
+    _close("rmsnorm dw", _np(w.grad), gdw, 1e-2, 2e-2)
+
+
+def test_swiglu_matches_oracle(gpu):
+    g = torch.Generator(device=gpu).manual_seed(7)
+    gu = (torch.randn(64, 2 * 12288, device=gpu, generator=g) * 2).to(torch.bfloat16).requires_grad_()
+    out = swiglu(gu)
+    d = torch.randn(out.shape, device=gpu, generator=g).to(torch.bfloat16)
+    out.backward(d)
+    _close("swiglu out", _np(out), ol.swiglu(_np(gu)), 1e-2, 1e-2)
+    _close("swiglu dgu", _np(gu.grad), ol.swiglu_grad(_np(gu), _np(d)), 1e-2, 2e-2)
+
+
+class _Params(torch.nn.Module):
+    def __init__(self, gpu):
+        super().__init__()
+        g = torch.Generator(device=gpu).manual_seed(11)
+        self.a = torch.nn.Parameter(torch.randn(1000, 37, device=gpu, generator=g).to(torch.bfloat16))
+        self.b = torch.nn.Parameter(torch.randn(513, device=gpu, generator=g).to(torch.bfloat16))
+        self.frozen = torch.nn.Parameter(torch.randn(9, device=gpu).to(torch.bfloat16), requires_grad=False)
+
+
+def test_fused_adamw_matches_oracle_with_clip_and_skip(gpu):
+    mod = _Params(gpu)
+    opt = FusedBF16Optimizer(mod, lr=1e-2, weight_decay=0.1, max_grad_norm=5.0, total_steps=10,
+                             warmup_ratio=0.2)
+    p0 = _np(torch.cat([mod.a.detach().reshape(-1), mod.b.detach().reshape(-1)]).float())
+    g = torch.Generator(device=gpu).manual_seed(12)
+    grads, lrs = [], []
+    for step in range(4):
+        opt.zero_grad()
+        ga = torch.randn(mod.a.shape, device=gpu, generator=g) * (0.05 if step != 2 else 3.0)
+        gb = torch.randn(mod.b.shape, device=gpu, generator=g) * 0.05
+        if step == 1:
+            gb[5] = float("nan")  # a non-finite step: skipped
+        (mod.a * ga.to(torch.bfloat16)).sum().backward()
+        (mod.b * gb.to(torch.bfloat16)).sum().backward()
+        assert mod.a.grad.data_ptr() == opt.grads.data_ptr()  # accumulated in place
+        grads.append(_np(torch.cat([mod.a.grad.reshape(-1), mod.b.grad.reshape(-1)])))
+        lrs.append(opt.get_learning_rate())
+        norm = opt.step()
+        want_p, want_norms, want_t = ol.adamw_steps(p0, grads, lrs=lrs, weight_decay=0.1, max_grad_norm=5.0)
+        got = _np(opt.master[: p0.size])
+        print(f"step {step}: lr={lrs[-1]:.3e} norm={float(norm):.4f} oracle={want_norms[-1]:.4f}")
+        if np.isfinite(want_norms[-1]):
+            assert float(norm) == pytest.approx(want_norms[-1], rel=1e-4)
+        else:
+            assert not np.isfinite(float(norm))
+        np.testing.assert_allclose(got, want_p[-1], rtol=1e-5, atol=1e-6)
+        np.testing.assert_array_equal(_np(mod.a).reshape(-1), _np(opt.master[: mod.a.numel()].to(torch.bfloat16)))
+    assert opt.optimizer_steps() == 3
+    assert lrs == [warmup_decay_lr(i, max_lr=1e-2, total_steps=10, warmup_steps=2) for i in range(4)]
+
+
+def _small_model(gpu, seed=0):
+    return DSparkDraftLayerModel(hidden=256, heads=4, kv_heads=2, head_dim=128, ffn=512, vocab=700,
+                                 draft_vocab=300, max_positions=512, device=gpu, seed=seed)
+
+
+def test_layer_forward_and_gradients_match_oracle(gpu):
+    model = _small_model(gpu)
+    w = W.from_layout("small", [150, 106], np.array([0, 40, 96, 150, 190]), np.array([0, 0, 0, 1, 1]), 16)
+    batch = layer_batch(model, w, seed=5)
+    hidden = model(batch["target_hidden"], batch["draft_input_ids"], batch["context_positions"],
+                   batch["draft_positions"], batch["metadata"])
+    G = torch.randn(hidden.shape, device=gpu, generator=torch.Generator(device=gpu).manual_seed(9))
+    hidden.backward(G.to(hidden.dtype))
+    names = [n for n, p in model.named_parameters()]
+    P = {n: torch.tensor(_np(p), requires_grad=p.requires_grad) for n, p in model.named_parameters()}
+    ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
+                       w.block_size, w.sequence_length)
+    visible = M.endpoints_to_dense(ends, w.num_keys)
+    ref = ol.layer_forward(P, _np(batch["target_hidden"]), batch["draft_input_ids"].cpu().numpy(),
+                           batch["context_positions"].cpu().numpy(), batch["draft_positions"].cpu().numpy(),
+                           visible, _np(model.rope_cos), _np(model.rope_sin), model.eps)
+    (ref * torch.as_tensor(_np(G.to(hidden.dtype)))).sum().backward()
+    _close("layer hidden", _np(hidden), ref.detach().numpy(), 3e-2, 6e-2)
+    for n, p in model.named_parameters():
+        if not p.requires_grad:
+            continue
+        _close(f"grad {n}", _np(p.grad), P[n].grad.numpy(), 5e-2, 0.15)
+    assert len(names) == len(P)
+
+
+def test_layer_step_loss_matches_oracle(gpu):
+    model = _small_model(gpu, seed=1)
+    opt = FusedBF16Optimizer(model, lr=1e-3, total_steps=100, warmup_ratio=0.0)
+    w = W.from_layout("small", [150, 106], np.array([0, 40, 96, 150, 190]), np.array([0, 0, 0, 1, 1]), 16)
+    batch = layer_batch(model, w, seed=6)
+    params_before = {n: _np(p) for n, p in model.named_parameters()}
+    loss, norm = dspark_layer_step(model, opt, batch)
+    ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
+                       w.block_size, w.sequence_length)
+    visible = M.endpoints_to_dense(ends, w.num_keys)
+    P = {n: torch.tensor(v) for n, v in params_before.items()}
+    hidden = ol.layer_forward(P, _np(batch["target_hidden"]), batch["draft_input_ids"].cpu().numpy(),
+                              batch["context_positions"].cpu().numpy(), batch["draft_positions"].cpu().numpy(),
+                              visible, _np(model.rope_cos), _np(model.rope_sin), model.eps).numpy()
+    head = params_before["lm_head"]
+    logits = hidden @ head.T
+    teacher = (_np(batch["teacher_hidden"]).reshape(-1, head.shape[1]) @ head.T)
+    t = batch["targets"]
+    tgt = t.target_ids.reshape(-1).cpu().numpy()
+    tidx = t.teacher_index.reshape(-1).cpu().numpy()
+    wts = t.weights.reshape(-1).cpu().numpy().astype(np.float64)
+    ce = oloss.cross_entropy(logits, tgt)
+    l1 = oloss.l1(logits, teacher[np.clip(tidx, 0, None)])
+    ref = (0.1 * (ce * wts).sum() + 0.9 * (l1 * wts).sum()) / max(wts.sum(), 1e-6)
+    print(f"layer step loss: got={float(loss):.6f} oracle={ref:.6f} grad_norm={float(norm):.4f}")
+    assert float(loss) == pytest.approx(ref, rel=2e-2)
+    assert opt.optimizer_steps() == 1
+    moved = [n for n, p in model.named_parameters() if p.requires_grad
+             and not np.array_equal(_np(p), params_before[n])]
+    assert "q_proj" in moved and "down_proj" in moved
+
+
+def test_config5_full_geometry_steps(gpu):
+    model = DSparkDraftLayerModel(device=gpu)
+    opt = FusedBF16Optimizer(model, lr=1e-4, total_steps=1000, warmup_ratio=0.0)
+    batch = layer_batch(model, W.config5(), seed=0)
+    q0 = model.q_proj.detach().clone()
+    losses = []
+    for _ in range(3):
+        loss, norm = dspark_layer_step(model, opt, batch)
+        losses.append(float(loss))
+        assert np.isfinite(float(norm))
+    print(f"config5 losses: {losses}")
+    assert all(np.isfinite(losses))
+    assert opt.optimizer_steps() == 3
+    assert not torch.equal(q0, model.q_proj.detach())

@@ -1,0 +1,116 @@
+"""Pins the one-layer step oracle (oracle/layer.py) against closed forms and finite differences
+(CPU only)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import layer as ol
+
+
+def _rng(seed=0):
+    return np.random.default_rng(seed)
+
+
+def test_rms_norm_constant_rows_normalise_to_the_weight():
+    w = np.array([0.5, -2.0, 3.0, 1.0])
+    for c in (-3.0, 0.25, 7.0):
+        _, out = ol.rms_norm(np.full((2, 4), c), w, eps=0.0)
+        np.testing.assert_allclose(out, np.sign(c) * np.broadcast_to(w, (2, 4)), rtol=1e-14)
+
+
+def test_rms_norm_residual_is_added_first():
+    r = _rng(1)
+    x, res, w = r.standard_normal((3, 8)), r.standard_normal((3, 8)), r.standard_normal(8)
+    y, out = ol.rms_norm(x, w, 1e-6, residual=res)
+    np.testing.assert_allclose(y, x + res)
+    np.testing.assert_allclose(out, ol.rms_norm(x + res, w, 1e-6)[1])
+
+
+def test_rms_norm_gradients_match_finite_differences():
+    r = _rng(2)
+    y, w, g, extra = (r.standard_normal((3, 6)), r.standard_normal(6), r.standard_normal((3, 6)),
+                      r.standard_normal((3, 6)))
+    eps = 1e-5
+    dy, dw = ol.rms_norm_grad(y, w, eps, g, dy_extra=extra)
+    f = lambda y_, w_: float((g * ol.rms_norm(y_, w_, eps)[1]).sum() + (extra * y_).sum())
+    h = 1e-6
+    fd_y = np.zeros_like(y)
+    for i in np.ndindex(y.shape):
+        a, b = y.copy(), y.copy()
+        a[i] += h
+        b[i] -= h
+        fd_y[i] = (f(a, w) - f(b, w)) / (2 * h)
+    fd_w = np.zeros_like(w)
+    for i in range(w.size):
+        a, b = w.copy(), w.copy()
+        a[i] += h
+        b[i] -= h
+        fd_w[i] = (f(y, a) - f(y, b)) / (2 * h)
+    np.testing.assert_allclose(dy, fd_y, rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(dw, fd_w, rtol=1e-6, atol=1e-8)
+
+
+def test_swiglu_special_values_and_gradient():
+    gu = np.array([[0.0, 50.0, -50.0, 2.0, 3.0, 4.0]])
+    out = ol.swiglu(gu)
+    # silu(0) = 0, silu(50) -> 50, silu(-50) -> 0
+    np.testing.assert_allclose(out, [[0.0, 50.0 * 3.0, 0.0]], atol=1e-12)
+    r = _rng(3)
+    gu = r.standard_normal((2, 8))
+    d = r.standard_normal((2, 4))
+    grad = ol.swiglu_grad(gu, d)
+    h = 1e-6
+    fd = np.zeros_like(gu)
+    for i in np.ndindex(gu.shape):
+        a, b = gu.copy(), gu.copy()
+        a[i] += h
+        b[i] -= h
+        fd[i] = ((d * ol.swiglu(a)).sum() - (d * ol.swiglu(b)).sum()) / (2 * h)
+    np.testing.assert_allclose(grad, fd, rtol=1e-6, atol=1e-8)
+
+
+def test_adamw_first_step_closed_form_and_clip():
+    p0 = np.array([1.0, -2.0, 0.5])
+    g = np.array([0.1, -0.2, 0.0])
+    lr, wd, eps = 1e-2, 0.1, 1e-8
+    out, norms, t = ol.adamw_steps(p0, [g], lrs=[lr], weight_decay=wd, eps=eps, max_grad_norm=10.0)
+    # fresh state: m_hat = g, v_hat = g^2, so the step is lr * g / (|g| + eps) after the decay
+    want = p0 * (1 - lr * wd) - lr * g / (np.abs(g) + eps)
+    np.testing.assert_allclose(out[0], want, rtol=1e-12)
+    assert norms[0] == pytest.approx(math.sqrt(0.05))
+    assert t == 1
+    # a clipped gradient takes the same first step direction (the ratio is scale free) ...
+    clipped, _, _ = ol.adamw_steps(p0, [g], lrs=[lr], weight_decay=wd, eps=0.0, max_grad_norm=1e-3)
+    np.testing.assert_allclose(clipped[0][:2], (p0 * (1 - lr * wd) - lr * np.sign(g))[:2], rtol=1e-12)
+    # ... and a non-finite gradient skips the step entirely
+    skipped, _, t2 = ol.adamw_steps(p0, [np.array([np.nan, 0.0, 0.0]), g], lrs=[lr, lr])
+    np.testing.assert_array_equal(skipped[0], p0)
+    assert t2 == 1
+
+
+def test_layer_forward_is_differentiable_and_row_local():
+    """The oracle layer runs in fp64 with autograd; a draft query whose only visible keys are its
+    own block does not see the context."""
+    r = _rng(4)
+    H, D, hq, hkv, F, T, nq, V = 16, 8, 2, 1, 32, 6, 4, 20
+    params = {
+        "embed_tokens": r.standard_normal((V, H)), "context_proj": r.standard_normal((H, 3 * H)) * 0.1,
+        "context_norm": np.ones(H), "input_layernorm": np.ones(H), "q_proj": r.standard_normal((hq * D, H)),
+        "k_proj": r.standard_normal((hkv * D, H)), "v_proj": r.standard_normal((hkv * D, H)),
+        "q_norm": np.ones(D), "k_norm": np.ones(D), "o_proj": r.standard_normal((H, hq * D)) * 0.1,
+        "post_attention_layernorm": np.ones(H), "gate_up_proj": r.standard_normal((2 * F, H)) * 0.1,
+        "down_proj": r.standard_normal((H, F)) * 0.1, "final_norm": np.ones(H)}
+    P = {k: torch.tensor(v, requires_grad=True) for k, v in params.items()}
+    th = r.standard_normal((1, T, 3 * H))
+    vis = np.zeros((nq, T + nq), bool)
+    vis[:, T:] = True  # draft-only visibility
+    cos, sin = np.ones((16, D)), np.zeros((16, D))
+    out = ol.layer_forward(P, th, [1, 2, 3, 4], np.arange(T), np.arange(nq), vis, cos, sin, 1e-6)
+    out.sum().backward()
+    assert P["context_proj"].grad is not None
+    # keys of the context are masked: the context projection receives no gradient through attention
+    assert float(P["context_proj"].grad.abs().max()) == 0.0
+    assert float(P["q_proj"].grad.abs().max()) > 0.0
