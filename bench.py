@@ -16,6 +16,9 @@ Row-level operations that run once per row outside the step (packing collator, d
 sampler) and the fused Q/K RMSNorm + RoPE of the draft layer (fwd + bwd at the config-2 geometry;
 config 2's step starts from projected Q/K/V) are timed separately and reported with
 "outside_step": true.
+After the main measurement the full one-layer DSpark training step of BASELINE config 5 (forward,
+loss, backward and the fused AdamW) is timed on its own and reported under "config5_layer_step"
+(skip with --no-layer-step).
 Metric: input context tokens per second (4096 per step / wall time), as the reference's draft-only
 benchmark defines it (tools/performance/torchspec_benchmark.py:688,764).
 
@@ -51,6 +54,11 @@ def parse():
     p.add_argument("--no-kernel-timing", action="store_true", help="no per-kernel HIP events")
     p.add_argument("--no-gemm-tuning", action="store_true",
                    help="library-default GEMM solutions instead of the recorded TunableOp file")
+    p.add_argument("--no-layer-step", action="store_true",
+                   help="skip the config-5 one-layer training step measured after the main line")
+    p.add_argument("--layer-step-only", action="store_true",
+                   help="only time the config-5 one-layer training step and print its JSON object "
+                        "(for profiling it on its own)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (5 times): the reference kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -202,7 +210,7 @@ def kernel_work(w):
 # the head GEMMs are the library kernels the recorded TunableOp solutions select
 _REGION_KERNEL = {"attn_fwd": "attn_fwd_kernel<4>", "attn_bwd_dq": "attn_bwd_dq_kernel<4>",
                   "attn_bwd_dkdv": "attn_bwd_dkdv_kernel<4>", "attn_bwd_prepare": "attn_bwd_pre_kernel",
-                  "loss_fwd": "loss_fwd_persistent<8>", "loss_bwd": "loss_bwd_kernel<true>",
+                  "loss_fwd": "loss_fwd_persistent<8, false>", "loss_bwd": "loss_bwd_kernel<true>",
                   "head_gemm_fwd": "Custom_Cijk_Alik_Bljk_BBS_BH_MT256x256x64_MI16x16x1_UserArgs_shortname0_gfx950",
                   "qk_norm_rope_fwd": "qk_norm_rope_fwd_kernel", "qk_norm_rope_bwd": "qk_norm_rope_bwd_kernel"}
 _LIBRARY_REGIONS = ("head_gemm_fwd", "head_gemm_dgrad", "teacher_gemm")
@@ -321,6 +329,56 @@ def aux_qk(device, w, reps):
     return {k: (stats[k]["mean_ms"], stats[k]["launches"], work[k]) for k in work if k in stats}
 
 
+def layer_step(device, steps, warmup):
+    """BASELINE config 5, the full one-layer DSpark training step (Qwen3-8B dims: hidden 4096,
+    GQA 32/8 x 128, SwiGLU FFN 12288, RMSNorm, RoPE theta 1e6; 3 packed documents, 4096 tokens,
+    507 anchors x 16; forward + 0.1 CE + 0.9 L1 + backward + fused AdamW over 243M trainable
+    parameters), timed after the config-2 measurement. Returns its own step time, tokens/s and
+    per-region means."""
+    import torch
+
+    from aspec_amd import _timing
+    from aspec_amd import workloads as W
+    from aspec_amd.draft_layer import (DSparkDraftLayerModel, FusedBF16Optimizer, dspark_layer_step,
+                                       layer_batch)
+
+    model = DSparkDraftLayerModel(device=device)
+    opt = FusedBF16Optimizer(model, lr=1e-4, total_steps=10_000, warmup_ratio=0.0)
+    w5 = W.config5()
+    batch = layer_batch(model, w5, seed=0)
+    for _ in range(warmup):
+        dspark_layer_step(model, opt, batch)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss, norm = dspark_layer_step(model, opt, batch)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    if not (torch.isfinite(loss) and torch.isfinite(norm)):
+        raise RuntimeError("non-finite loss or gradient norm in the config-5 steps")
+    _timing.reset()
+    _timing.enable(True)
+    for _ in range(min(steps, 5)):
+        dspark_layer_step(model, opt, batch)
+    torch.cuda.synchronize()
+    _timing.enable(False)
+    stats = _timing.summary()
+    n = opt.flat.numel()
+    adam_bytes = n * 30  # bf16 grads read twice (norm, update), fp32 master/m/v read + written, bf16 param written
+    regions = {k: round(v["mean_ms"], 4) for k, v in stats.items()}
+    out = {"workload": f"config5: one DSpark draft layer, {len(w5.lengths)} documents {w5.lengths}, "
+                       f"{w5.num_blocks} anchors x {w5.block_size}, trainable params {n}",
+           "ms_per_step": round(elapsed * 1e3 / steps, 3),
+           "tokens_per_s": round(w5.context_length * steps / elapsed, 1),
+           "final_loss": round(float(loss), 5), "regions_ms": regions}
+    if "adamw_step" in stats:
+        gbs = adam_bytes / (stats["adamw_step"]["mean_ms"] * 1e-3) / 1e9
+        out["adamw"] = {"bytes": adam_bytes, "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+    del model, opt, batch
+    torch.cuda.empty_cache()
+    return out
+
+
 def measured_traffic(region):
     """HBM bytes per launch (read + write) of a region's kernel, from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
@@ -409,6 +467,9 @@ def main():
 
     _lib.load()  # fail loudly if the HIP library is missing
     device = torch.device("cuda:0")
+    if args.layer_step_only:
+        print(json.dumps({"config5_layer_step": layer_step(device, args.steps, args.warmup)}), flush=True)
+        return
     x = build_inputs(device, args.seed)
     head_fn = _Head.make()
     w = x["w"]
@@ -504,6 +565,8 @@ def main():
         "kernels": per_kernel,
         "cpu_baseline": None,
     }
+    if not args.no_layer_step:
+        result["config5_layer_step"] = layer_step(device, max(3, args.steps // 2), 2)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(x, args.seed)
     print(json.dumps(result), flush=True)

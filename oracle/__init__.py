@@ -20,6 +20,10 @@ How each part is pinned (besides agreeing with the HIP path):
   qk_norm_rope.py -- RMSNorm and RoPE closed forms: constant rows normalize to +-1, cos=1/sin=0
                   is the identity, cos=0/sin=1 is rotate_half, the rotation keeps each (i, i+D/2)
                   pair's norm, and finite-difference gradients.
+  layer.py     -- RMSNorm of constant rows gives +-w and its residual add comes first; RMSNorm and
+                  SwiGLU gradients against finite differences; AdamW's closed-form first step,
+                  clipping and non-finite skip; the fp64 one-layer forward is differentiable and
+                  respects the mask.
   dspark_head.py -- the Markov logits reduce to h W^T for w2 = 0 and to a w2 column for a one-hot
                   w1 row; argmax against hand-stated indices (ties, NaN, +-inf rows); acceptance
                   statistics against a hand-computed block; BCE at 0 and its gradient; the Markov
