@@ -602,31 +602,41 @@ __device__ __forceinline__ void mfma_tr_32(f32x16 (&acc)[4], const uint16_t* til
 
 // P wave: S, masked P (to LDS for the dS wave) and dV += P^T dO for one stage. Rows at or past
 // `valid` hold copies of a real row and get an empty mask. `key_base` is the slice's first key.
+// A fully visible stage (a full tile with all rows real) skips the visibility words and the mask.
 __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf16x8 (&kf)[8],
                                             f32x16 (&dvacc)[4], float scale_log2, int w, int valid,
-                                            int key_base, int ro, const TrOffsets& tro, int lane) {
+                                            bool all_visible, int key_base, int ro,
+                                            const TrOffsets& tro, int lane) {
   const int g = lane >> 5;
   const int c = lane & 31;
-  if (lane < kBwdTileM) {  // visibility word of row `lane` for this slice
-    const uint32_t bits = interval_bits(s.ends[0][lane], s.ends[1][lane], key_base) |
-                          interval_bits(s.ends[2][lane], s.ends[3][lane], key_base);
-    s.mask[w][lane] = lane < valid ? bits : 0u;
+  if (!all_visible) {
+    if (lane < kBwdTileM) {  // visibility word of row `lane` for this slice
+      const uint32_t bits = interval_bits(s.ends[0][lane], s.ends[1][lane], key_base) |
+                            interval_bits(s.ends[2][lane], s.ends[3][lane], key_base);
+      s.mask[w][lane] = lane < valid ? bits : 0u;
+    }
+    __builtin_amdgcn_wave_barrier();
   }
-  __builtin_amdgcn_wave_barrier();
   f32x16 sacc = mfma_chain_lds_reg(RowOperand{s.q, ro}, kf);  // rows: queries, lane: key
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq) {
     const int r0 = rq * 8 + g * 4;
     const f32x4 l4 = *reinterpret_cast<const f32x4*>(s.lse2 + r0);
-    const u32x4 m4 = *reinterpret_cast<const u32x4*>(&s.mask[w][r0]);
     f32x4 p4;
+    if (all_visible) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float p = fast_exp2(sacc[rq * 4 + j] * scale_log2 - l4[j]);
-      const int keep = __builtin_amdgcn_sbfe(static_cast<int>(m4[j]), c, 1);  // 0 or -1
-      p4[j] = __int_as_float(__float_as_int(p) & keep);
-      sacc[rq * 4 + j] = p4[j];
+      for (int j = 0; j < 4; ++j) p4[j] = fast_exp2(sacc[rq * 4 + j] * scale_log2 - l4[j]);
+    } else {
+      const u32x4 m4 = *reinterpret_cast<const u32x4*>(&s.mask[w][r0]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p = fast_exp2(sacc[rq * 4 + j] * scale_log2 - l4[j]);
+        const int keep = __builtin_amdgcn_sbfe(static_cast<int>(m4[j]), c, 1);  // 0 or -1
+        p4[j] = __int_as_float(__float_as_int(p) & keep);
+      }
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sacc[rq * 4 + j] = p4[j];
     px.p[w][rq][lane] = p4;
   }
   const bf16x8 pp[2] = {pack_c_half(sacc, 0), pack_c_half(sacc, 8)};
@@ -731,7 +741,7 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   const int64_t key0 = n * kBwdTileN;
   // The unit's (at most 32) query tiles, one per lane, read with readlane in the loop: no memory
   // access there besides the stage loads.
-  const int my_tile = lane < last - first ? list[first + lane] & ~kFullBit : 0;
+  const int my_tile = lane < last - first ? list[first + lane] : 0;  // query tile | kFullBit
 
   // This wave's B operand for the whole walk: K (P waves) or V (dS waves) rows of its 32 keys.
   const int64_t key = key0 + w * 32 + c;
@@ -751,7 +761,7 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   const int lcol = ((lane & 15) ^ swz(lrow)) * 8;
   const bool three_loads = wave < 3;
   auto row_base = [&](int it, int64_t& q0, int& head, int& valid) {
-    q0 = static_cast<int64_t>(__builtin_amdgcn_readlane(my_tile, it / G)) * kBwdTileM;
+    q0 = static_cast<int64_t>(__builtin_amdgcn_readlane(my_tile, it / G) & ~kFullBit) * kBwdTileM;
     head = hkv * G + it % G;
     valid = static_cast<int>(min<int64_t>(kBwdTileM, a.nq - q0));
   };
@@ -810,8 +820,10 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
       int64_t q0;
       int head, valid;
       row_base(i, q0, head, valid);
+      const bool full = (static_cast<uint32_t>(__builtin_amdgcn_readlane(my_tile, i / G)) & kFullBit) != 0;
       dkdv_p_step(live ? s_cur : st3, x_cur, kvf, acc, a.scale_log2, w, live ? valid : 0,
-                  static_cast<int>(key0) + w * 32, ro_t, tro_t, lane);
+                  live && full && valid == kBwdTileM, static_cast<int>(key0) + w * 32, ro_t, tro_t,
+                  lane);
     } else {
       dkdv_ds_step(s_prv, x_prv, kvf, acc, w, ro_t, tro_t, lane);  // trip 0: stage 3 and buffer 1
     }
