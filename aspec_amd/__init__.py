@@ -2,8 +2,8 @@
 
 Drop-in replacements for the reference operators of aspec/models/ops (direct CP / THD attention,
 THD sparse metadata, tiled L1, the selective-head losses, the fused Q/K RMSNorm + RoPE, the DSpark
-head terms with the Markov bias and confidence head), the packing collator
-(aspec/data/utils.py), the anchor layout (anchors.py), output-block compaction (output_blocks.py)
+head terms with the Markov bias and confidence head), the work-aware row packing policy
+(aspec/controller/packing.py), the packing collator (aspec/data/utils.py), the anchor layout (anchors.py), output-block compaction (output_blocks.py)
 and the DSpark targets (dspark.py), backed by hand-written HIP kernels in libaspec_amd.so,
 reached through the C ABI of include/aspec_amd.h.
 """
@@ -35,6 +35,12 @@ from aspec_amd.dspark_qk_norm_rope import (  # noqa: F401
     dspark_qk_norm_rope,
     dspark_qk_norm_rope_available,
 )
+from aspec_amd.packing import (  # noqa: F401
+    PackingResult,
+    count_eligible_anchor_starts,
+    count_eligible_anchor_starts_batch,
+    pack_work_aware_rows,
+)
 from aspec_amd.targets import decay_weights, dspark_targets  # noqa: F401
 from aspec_amd.output_blocks import (  # noqa: F401
     output_block_counts,
@@ -51,6 +57,10 @@ from aspec_amd.tiled_l1 import tiled_l1_from_logits  # noqa: F401
 __all__ = [
     "AcceptRatePredictor",
     "DFlashPackingCollator",
+    "PackingResult",
+    "count_eligible_anchor_starts",
+    "count_eligible_anchor_starts_batch",
+    "pack_work_aware_rows",
     "VanillaMarkov",
     "acceptance_statistics",
     "build_markov_head",

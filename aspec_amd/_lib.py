@@ -97,9 +97,11 @@ SIGNATURES = {
         _int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p] + [_i64] * 5
         + [_c_void_p] * 8
     ),
+    "aspec_count_eligible_anchor_starts": (_int, [_c_void_p] * 3 + [_i64, _i64, _c_void_p]),
+    "aspec_pack_work_aware_rows": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib = None

@@ -1,7 +1,8 @@
 """Builds libaspec_amd.so (all HIP kernels + the C ABI) for gfx950 with hipcc, in-tree.
 
-Every `csrc/*.hip` file compiles to an object under `_build/` (in parallel), then one link step
-produces `aspec_amd/libaspec_amd.so`, which travels with the source tree.
+Every `csrc/*.hip` file compiles to an object under `_build/` (in parallel), host-only
+`csrc/*.cpp` files compile with the host C++ compiler, then one link step produces
+`aspec_amd/libaspec_amd.so`, which travels with the source tree.
 """
 
 from __future__ import annotations
@@ -43,16 +44,29 @@ def hipcc() -> str:
     return path
 
 
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall"]
+
+
+def host_cxx() -> str:
+    path = shutil.which("g++") or shutil.which("c++")
+    if path is None:
+        raise RuntimeError("no host C++ compiler found for the host-only sources")
+    return path
+
+
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, *PER_FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+    if src.suffix == ".cpp":
+        cmd = [host_cxx(), *HOST_FLAGS, "-c", str(src), "-o", str(obj)]
+    else:
+        cmd = [hipcc(), *COMMON_FLAGS, *PER_FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src.name}:\n{err}")
+        raise RuntimeError(f"{Path(cmd[0]).name} failed for {src.name}:\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
     return obj
@@ -61,7 +75,7 @@ def _compile(src: Path, verbose: bool) -> Path:
 def build(verbose: bool = False) -> Path:
     """Compile every HIP source and link libaspec_amd.so. Always rebuilds."""
     BUILD_DIR.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     jobs = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))

@@ -427,6 +427,36 @@ int aspec_adamw_step(void* params, float* master, float* exp_avg, float* exp_avg
                      float beta2, float eps, float max_grad_norm, void* state, void* workspace,
                      void* stream);
 
+/* ---- Row packing policy (host only: plain host arrays, no GPU, no stream) ---- */
+
+/*
+ * Useful anchor starts per pooled sample: count_eligible_anchor_starts
+ * (aspec/controller/packing.py:43-67), batched. Sample s has run lengths
+ * runs[run_offsets[s] .. run_offsets[s+1]) of its packed loss mask (alternating unsupervised /
+ * supervised, unsupervised first) and length sample_lengths[s]; counts_out[s] is the number of
+ * supervised positions p with p <= length - block_size (0 when length or block_size is not
+ * positive). A negative run length is an error.
+ */
+int aspec_count_eligible_anchor_starts(const int64_t* runs, const int64_t* run_offsets,
+                                       const int64_t* sample_lengths, int64_t num_samples,
+                                       int64_t block_size, int64_t* counts_out);
+
+/*
+ * Work-aware row packing: pack_work_aware_rows (aspec/controller/packing.py:87-167). Samples
+ * 0..dp_size-1 seed one row each; the rest, by useful_work/length (double quotient), useful_work and
+ * length (descending) and index, go to the fitting row with the least slack (ties: lower row) until
+ * max_selected samples are taken (max_selected < 0: no limit; otherwise >= dp_size). Rows come out
+ * ordered by tokens, descending (ties: lower row): row k holds
+ * row_samples[row_offsets[k] .. row_offsets[k+1]) in placement order, row_tokens_out[k] tokens.
+ * row_offsets [dp_size + 1], row_samples [count], row_tokens_out [dp_size].
+ * count < dp_size packs nothing (row_offsets all 0: the reference returns None). Errors: lengths
+ * outside [1, max_seq_length] (message names the first), non-positive dp_size / max_seq_length,
+ * max_selected below dp_size, lengths or useful_work beyond 2^53.
+ */
+int aspec_pack_work_aware_rows(const int64_t* lengths, const int64_t* useful_work, int64_t count,
+                               int64_t dp_size, int64_t max_seq_length, int64_t max_selected,
+                               int64_t* row_offsets, int64_t* row_samples, int64_t* row_tokens_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,6 +24,9 @@ How each part is pinned (besides agreeing with the HIP path):
                   SwiGLU gradients against finite differences; AdamW's closed-form first step,
                   clipping and non-finite skip; the fp64 one-layer forward is differentiable and
                   respects the mask.
+  packing.py   -- the reference's own packing test cases with hand-derived placements, brute-force
+                  eligible anchor starts, exact-double density ties, and a replay of every
+                  placement (best fit, skips, seeds, capacity, rank order) on random pools.
   dspark_head.py -- the Markov logits reduce to h W^T for w2 = 0 and to a w2 column for a one-hot
                   w1 row; argmax against hand-stated indices (ties, NaN, +-inf rows); acceptance
                   statistics against a hand-computed block; BCE at 0 and its gradient; the Markov
