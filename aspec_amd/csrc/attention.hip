@@ -25,6 +25,9 @@ constexpr int kUnitChunkBits = 12;
 // Online softmax keeps a stale row maximum until a tile raises it by more than 2^8: exp2 of the
 // shifted scores stays <= 256 (exact in fp32, fine in bf16) and O is rescaled only then.
 constexpr float kRescaleThreshold = 8.f;
+// LDS read-ahead (k-steps) of the score chains of the forward and dQ kernels.
+constexpr int kFwdAhead = 1;
+constexpr int kDqAhead = 1;
 
 struct AttnArgs {
   const uint16_t* q; int64_t qst, qsh;
@@ -69,50 +72,53 @@ __device__ __forceinline__ void load_row_frag(bf16x8 (&frag)[8], const uint16_t*
   }
 }
 
-// The MFMA chains below load their LDS operands one k-step ahead and fence each step with a
+// The MFMA chains below load their LDS operands a few k-steps ahead and fence each step with a
 // scheduling barrier: without it the scheduler hoists every LDS read of the tile to the top,
 // which overflows the VGPR budget and parks operands in AGPRs.
 #define ASPEC_STEP_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-// Two independent 8-step chains: acc0 += A0 x B0, acc1 += A1 x B1 over the 128-dim reduction.
-// A rows live in LDS (`ra0` / `ra1`); the B operands come from registers (`b0`, `b1`) or, when
-// null, from LDS rows `rb0` / `rb1`.
+// Two independent 8-step chains: acc0 = A0 x B0, acc1 = A1 x B1 over the 128-dim reduction. A rows
+// live in LDS (`ra0` / `ra1`), read AHEAD k-steps ahead of their MFMA; the B operands come from
+// registers.
+template <int AHEAD>
 __device__ __forceinline__ void mfma_chains2(f32x16& acc0, f32x16& acc1, const RowOperand& ra0,
-                                             const RowOperand& ra1, const bf16x8* b0,
-                                             const bf16x8* b1, const RowOperand& rb0,
-                                             const RowOperand& rb1) {
+                                             const RowOperand& ra1, const bf16x8 (&b0)[8],
+                                             const bf16x8 (&b1)[8]) {
   acc0 = f32x16{};
   acc1 = f32x16{};
-  uint4 a0 = ra0.step(0), a1 = ra1.step(0);
-  uint4 x0 = b0 ? uint4{} : rb0.step(0), x1 = b1 ? uint4{} : rb1.step(0);
+  uint4 x0[8], x1[8];
+#pragma unroll
+  for (int ds = 0; ds < AHEAD; ++ds) {
+    x0[ds] = ra0.step(ds);
+    x1[ds] = ra1.step(ds);
+  }
 #pragma unroll
   for (int ds = 0; ds < 8; ++ds) {
-    uint4 na0{}, na1{}, nx0{}, nx1{};
-    if (ds < 7) {
-      na0 = ra0.step(ds + 1);
-      na1 = ra1.step(ds + 1);
-      if (!b0) nx0 = rb0.step(ds + 1);
-      if (!b1) nx1 = rb1.step(ds + 1);
+    if (ds + AHEAD < 8) {
+      x0[ds + AHEAD] = ra0.step(ds + AHEAD);
+      x1[ds + AHEAD] = ra1.step(ds + AHEAD);
     }
-    acc0 = mfma32(as_bf16x8(a0), b0 ? b0[ds] : as_bf16x8(x0), acc0);
-    acc1 = mfma32(as_bf16x8(a1), b1 ? b1[ds] : as_bf16x8(x1), acc1);
+    acc0 = mfma32(as_bf16x8(x0[ds]), b0[ds], acc0);
+    acc1 = mfma32(as_bf16x8(x1[ds]), b1[ds], acc1);
     ASPEC_STEP_FENCE();
-    a0 = na0;
-    a1 = na1;
-    x0 = nx0;
-    x1 = nx1;
   }
+}
+
+// First k-step fragments of mfma_tr_blocks, read early so that their latency hides under the
+// caller's softmax work.
+__device__ __forceinline__ void read_tr_first(bf16x8 (&cur)[4], const uint16_t* tile, const TrOffsets& tro) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) cur[d] = read_tr_operand(tile, tro, 0, d * 32);
 }
 
 // acc[d] += A(d, ks) x B[ks] for d = 0..3 and k-steps ks = 0..KS-1, where A(d, ks) is the
 // transposed fragment of the row-major LDS `tile` (rows = the reduction index, 16 per k-step;
-// columns d*32 .. +32 = the output rows), read with transpose loads.
+// columns d*32 .. +32 = the output rows), read with transpose loads; `cur` holds k-step 0
+// (read_tr_first).
 template <int KS>
 __device__ __forceinline__ void mfma_tr_blocks(f32x16 (&acc)[4], const uint16_t* tile,
-                                               const TrOffsets& tro, const bf16x8 (&b)[KS]) {
-  bf16x8 cur[4];
-#pragma unroll
-  for (int d = 0; d < 4; ++d) cur[d] = read_tr_operand(tile, tro, 0, d * 32);
+                                               const TrOffsets& tro, bf16x8 (&cur)[4],
+                                               const bf16x8 (&b)[KS]) {
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     bf16x8 nxt[4];
@@ -248,9 +254,9 @@ __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
                                          float& l_run, bool partial, const RowIntervals& iv, float scale_log2,
                                          int ro, const TrOffsets& tro, int g) {
   f32x16 s[2];
-  const RowOperand none{nullptr, 0};
-  mfma_chains2(s[0], s[1], RowOperand{sk, ro}, RowOperand{sk + 32 * kRowLd, ro}, qf, qf, none,
-               none);
+  mfma_chains2<kFwdAhead>(s[0], s[1], RowOperand{sk, ro}, RowOperand{sk + 32 * kRowLd, ro}, qf, qf);
+  bf16x8 vcur[4];
+  read_tr_first(vcur, sv, tro);
   // Row maximum of the raw scores (scale > 0 commutes with max); the scale then folds into the
   // exponent: p = exp2(s * scale*log2e - m).
   if (partial) {
@@ -292,7 +298,7 @@ __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
   pb[1] = pack_c_half(s[0], 8);
   pb[2] = pack_c_half(s[1], 0);
   pb[3] = pack_c_half(s[1], 8);
-  mfma_tr_blocks<4>(oacc, sv, tro, pb);
+  mfma_tr_blocks<4>(oacc, sv, tro, vcur, pb);
 }
 
 // Two K/V stages (64 KB) per workgroup, two workgroups per CU: the next tile streams into LDS
@@ -432,15 +438,16 @@ __device__ __forceinline__ void dq_tile(const uint16_t* sk, const uint16_t* sv,
                                         f32x16 (&dqacc)[4], float lse2, float delta, bool partial,
                                         const RowIntervals& iv, float scale_log2, int ro,
                                         const TrOffsets& tro, int g) {
-  const RowOperand none{nullptr, 0};
   const float neg_lse2 = -lse2;
   // One 32-key half at a time: dS of the half goes straight into dQ (8 registers of dS live).
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     bf16x8 dsb[2];
     f32x16 s, dp;
-    mfma_chains2(s, dp, RowOperand{sk + kb * 32 * kRowLd, ro}, RowOperand{sv + kb * 32 * kRowLd, ro},
-                 qf, df, none, none);
+    mfma_chains2<kDqAhead>(s, dp, RowOperand{sk + kb * 32 * kRowLd, ro},
+                           RowOperand{sv + kb * 32 * kRowLd, ro}, qf, df);
+    bf16x8 kcur[4];
+    read_tr_first(kcur, sk + kb * 32 * kRowLd, tro);
     if (partial) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = iv.visible(kb * 32 + c_row(r, g)) ? s[r] : -INFINITY;
@@ -452,7 +459,7 @@ __device__ __forceinline__ void dq_tile(const uint16_t* sk, const uint16_t* sv,
     }
     dsb[0] = pack_c_half(s, 0);
     dsb[1] = pack_c_half(s, 8);
-    mfma_tr_blocks<2>(dqacc, sk + kb * 32 * kRowLd, tro, dsb);
+    mfma_tr_blocks<2>(dqacc, sk + kb * 32 * kRowLd, tro, kcur, dsb);
   }
 }
 
@@ -617,28 +624,34 @@ __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf1
     }
     __builtin_amdgcn_wave_barrier();
   }
+  // The row scalars are read before the S chain, so their latency hides under it; the softmax
+  // then runs as one straight-line block per case (the visibility words, needed only by partial
+  // stages, are read after the chain: holding them across it costs the chain its read-ahead).
+  f32x4 l4[4];
+#pragma unroll
+  for (int rq = 0; rq < 4; ++rq) l4[rq] = *reinterpret_cast<const f32x4*>(s.lse2 + rq * 8 + g * 4);
   f32x16 sacc = mfma_chain_lds_reg(RowOperand{s.q, ro}, kf);  // rows: queries, lane: key
+  if (all_visible) {
 #pragma unroll
-  for (int rq = 0; rq < 4; ++rq) {
-    const int r0 = rq * 8 + g * 4;
-    const f32x4 l4 = *reinterpret_cast<const f32x4*>(s.lse2 + r0);
-    f32x4 p4;
-    if (all_visible) {
+    for (int rq = 0; rq < 4; ++rq)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) p4[j] = fast_exp2(sacc[rq * 4 + j] * scale_log2 - l4[j]);
-    } else {
-      const u32x4 m4 = *reinterpret_cast<const u32x4*>(&s.mask[w][r0]);
+      for (int j = 0; j < 4; ++j) sacc[rq * 4 + j] = fast_exp2(sacc[rq * 4 + j] * scale_log2 - l4[rq][j]);
+  } else {
+    u32x4 m4[4];
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) m4[rq] = *reinterpret_cast<const u32x4*>(&s.mask[w][rq * 8 + g * 4]);
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float p = fast_exp2(sacc[rq * 4 + j] * scale_log2 - l4[j]);
-        const int keep = __builtin_amdgcn_sbfe(static_cast<int>(m4[j]), c, 1);  // 0 or -1
-        p4[j] = __int_as_float(__float_as_int(p) & keep);
+        const float p = fast_exp2(sacc[rq * 4 + j] * scale_log2 - l4[rq][j]);
+        const int keep = __builtin_amdgcn_sbfe(static_cast<int>(m4[rq][j]), c, 1);  // 0 or -1
+        sacc[rq * 4 + j] = __int_as_float(__float_as_int(p) & keep);
       }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sacc[rq * 4 + j] = p4[j];
-    px.p[w][rq][lane] = p4;
   }
+#pragma unroll
+  for (int rq = 0; rq < 4; ++rq)
+    px.p[w][rq][lane] = f32x4{sacc[rq * 4 + 0], sacc[rq * 4 + 1], sacc[rq * 4 + 2], sacc[rq * 4 + 3]};
   const bf16x8 pp[2] = {pack_c_half(sacc, 0), pack_c_half(sacc, 8)};
   mfma_tr_32(dvacc, s.dout, tro, pp);
 }
