@@ -80,9 +80,9 @@ __device__ __forceinline__ void load_row_frag(bf16x8 (&frag)[8], const uint16_t*
 // Two independent 8-step chains: acc0 = A0 x B0, acc1 = A1 x B1 over the 128-dim reduction. A rows
 // live in LDS (`ra0` / `ra1`), read AHEAD k-steps ahead of their MFMA; the B operands come from
 // registers.
-template <int AHEAD>
-__device__ __forceinline__ void mfma_chains2(f32x16& acc0, f32x16& acc1, const RowOperand& ra0,
-                                             const RowOperand& ra1, const bf16x8 (&b0)[8],
+template <int AHEAD, typename Operand>
+__device__ __forceinline__ void mfma_chains2(f32x16& acc0, f32x16& acc1, const Operand& ra0,
+                                             const Operand& ra1, const bf16x8 (&b0)[8],
                                              const bf16x8 (&b1)[8]) {
   acc0 = f32x16{};
   acc1 = f32x16{};
@@ -102,6 +102,88 @@ __device__ __forceinline__ void mfma_chains2(f32x16& acc0, f32x16& acc1, const R
     acc1 = mfma32(as_bf16x8(x1[ds]), b1[ds], acc1);
     ASPEC_STEP_FENCE();
   }
+}
+
+// Per-lane LDS byte offsets of a wave's reads of one 64 x 128 K/V tile, computed once per kernel:
+// the row reads of k-step ds (`row`) and the transposed reads of column block d (`tr`, the two
+// halves). Everything else in those addresses (the stage, the 32-row half, the k-step row block)
+// is a compile-time constant that lands in the instructions' offset field, so the tile loop spends
+// no VALU on LDS addresses.
+struct TileOffsets {
+  uint32_t row[8];
+  uint32_t tr[4][2];
+  __device__ __forceinline__ explicit TileOffsets(int lane) {
+    const int ro = row_operand_off(lane & 31, lane >> 5);
+    const TrOffsets t(lane);
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) row[ds] = static_cast<uint32_t>(ro ^ (ds << 4)) * 2u;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      tr[d][0] = static_cast<uint32_t>(t.lo ^ (d * 32)) * 2u;
+      tr[d][1] = static_cast<uint32_t>(t.hi ^ (d * 32)) * 2u;
+    }
+  }
+};
+
+__device__ __forceinline__ const char* byte_ptr(const uint16_t* p) { return reinterpret_cast<const char*>(p); }
+
+// Row-major operand read through TileOffsets.
+struct RowOperandT {
+  const uint16_t* tile;
+  const TileOffsets& o;
+  __device__ __forceinline__ uint4 step(int ds) const {
+    return *reinterpret_cast<const uint4*>(byte_ptr(tile) + o.row[ds]);
+  }
+};
+
+// Transposed fragment (rows ks*16 .. +15, columns d*32 .. +31) read through TileOffsets.
+__device__ __forceinline__ bf16x8 read_tr_t(const uint16_t* tile, const TileOffsets& o, int ks, int d) {
+  const char* b = byte_ptr(tile) + ks * 16 * kRowLd * 2;
+  const s16x4 lo = ds_read_tr16(reinterpret_cast<const uint16_t*>(b + o.tr[d][0]));
+  const s16x4 hi = ds_read_tr16(reinterpret_cast<const uint16_t*>(b + o.tr[d][1]));
+  const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+  const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+  return as_bf16x8(uint4{l2.x, l2.y, h2.x, h2.y});
+}
+
+// acc[d] += A(d, ks) x B[ks] as mfma_tr_blocks, with the fragments read through TileOffsets;
+// `cur` holds k-step 0.
+template <int KS>
+__device__ __forceinline__ void mfma_tr_blocks_t(f32x16 (&acc)[4], const uint16_t* tile,
+                                                 const TileOffsets& o, bf16x8 (&cur)[4],
+                                                 const bf16x8 (&b)[KS]) {
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    bf16x8 nxt[4];
+    if (ks + 1 < KS) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) nxt[d] = read_tr_t(tile, o, ks + 1, d);
+    }
+#pragma unroll
+    for (int d = 0; d < 4; ++d) acc[d] = mfma32(cur[d], b[ks], acc[d]);
+    ASPEC_STEP_FENCE();
+    if (ks + 1 < KS) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) cur[d] = nxt[d];
+    }
+  }
+}
+
+// Sum of the 32 bf16 values of four packed operands (the rounded P that the P.V MFMAs use), two
+// at a time with the bf16 dot product against ones.
+__device__ __forceinline__ float sum_bf16(const bf16x8 (&pb)[4]) {
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2v;
+  const bf16x2v ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint4 v = __builtin_bit_cast(uint4, pb[i]);
+    acc0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.x), ones, acc0, false);
+    acc1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.y), ones, acc1, false);
+    acc0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.z), ones, acc0, false);
+    acc1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.w), ones, acc1, false);
+  }
+  return acc0 + acc1;
 }
 
 // First k-step fragments of mfma_tr_blocks, read early so that their latency hides under the
@@ -252,11 +334,12 @@ struct ListWindow {
 __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
                                          const bf16x8 (&qf)[8], f32x16 (&oacc)[4], float& m_run,
                                          float& l_run, bool partial, const RowIntervals& iv, float scale_log2,
-                                         int ro, const TrOffsets& tro, int g) {
+                                         const TileOffsets& o, int g) {
   f32x16 s[2];
-  mfma_chains2<kFwdAhead>(s[0], s[1], RowOperand{sk, ro}, RowOperand{sk + 32 * kRowLd, ro}, qf, qf);
+  mfma_chains2<kFwdAhead>(s[0], s[1], RowOperandT{sk, o}, RowOperandT{sk + 32 * kRowLd, o}, qf, qf);
   bf16x8 vcur[4];
-  read_tr_first(vcur, sv, tro);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) vcur[d] = read_tr_t(sv, o, 0, d);
   // Row maximum of the raw scores (scale > 0 commutes with max); the scale then folds into the
   // exponent: p = exp2(s * scale*log2e - m).
   if (partial) {
@@ -282,23 +365,20 @@ __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
     for (int d = 0; d < 4; ++d) oacc[d] *= alpha;
   }
   const float neg_m = -m_run;
-  float rowsum = 0.f;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = fast_exp2(fmaf(s[kb][r], scale_log2, neg_m));
-      s[kb][r] = p;
-      rowsum += p;
-    }
+    for (int r = 0; r < 16; ++r) s[kb][r] = fast_exp2(fmaf(s[kb][r], scale_log2, neg_m));
   }
-  l_run += rowsum;
   bf16x8 pb[4];
   pb[0] = pack_c_half(s[0], 0);
   pb[1] = pack_c_half(s[0], 8);
   pb[2] = pack_c_half(s[1], 0);
   pb[3] = pack_c_half(s[1], 8);
-  mfma_tr_blocks<4>(oacc, sv, tro, vcur, pb);
+  // The row sum is taken over the rounded P that the P.V product uses, so O is normalized by
+  // exactly the weights it was built from.
+  l_run += sum_bf16(pb);
+  mfma_tr_blocks_t<4>(oacc, sv, o, vcur, pb);
 }
 
 // Two K/V stages (64 KB) per workgroup, two workgroups per CU: the next tile streams into LDS
@@ -326,11 +406,11 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) {
   ListWindow lw{a.plan.f_list + m * a.plan.nnf, a.plan.f_cnt[m], 0, 0};
   lw.load(0, lane);
   const KvTileLanes lanes(lane);
-  auto issue = [&](uint32_t entry, int stage) {
+  auto issue = [&](uint32_t entry, KvStageFwd& stage) {
     const int key0 = static_cast<int>(entry & ~kFullBit) * kTN;
-    issue_kv_tile<G>(kbase, a.kst, vbase, a.vst, key0, nk, ring[stage], wave, lanes);
+    issue_kv_tile<G>(kbase, a.kst, vbase, a.vst, key0, nk, stage, wave, lanes);
   };
-  if (lw.count > 0) issue(lw.entry(0), 0);
+  if (lw.count > 0) issue(lw.entry(0), ring[0]);
 
   bf16x8 qf[8];
   load_row_frag(qf, a.q + qsafe * a.qst + head * a.qsh, valid_q, g);
@@ -341,28 +421,28 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) {
   f32x16 oacc[4] = {};
   float m_run = kMaskValue;
   float l_run = 0.f;
-  const int ro = row_operand_off(c, g);
-  const TrOffsets tro(lane);
+  const TileOffsets offs(lane);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   lds_barrier();
 
-  for (int t = 0; t < lw.count; ++t) {
+  // Tile t computes from ring[t % 2] while tile t+1 streams into the other stage; the loop is
+  // unrolled by two so that each stage's LDS address is a constant.
+  auto tile = [&](int t, const KvStageFwd& cur, KvStageFwd& nxt) __attribute__((always_inline)) {
     const uint32_t entry = lw.entry(t);
     if (t + 1 < lw.count) {
       if (t + 1 - lw.base == kWave) lw.load(t + 1, lane);  // nothing else in flight here
-      issue(lw.entry(t + 1), (t + 1) & 1);
+      issue(lw.entry(t + 1), nxt);
     }
-    const KvStageFwd& st = ring[t & 1];
-    int ro_t = ro;
-    TrOffsets tro_t = tro;
-    opaque(ro_t);
-    opaque(tro_t.lo);
-    opaque(tro_t.hi);
     RowIntervals iv;
     iv.at_tile(static_cast<int>((entry & ~kFullBit) * kTN), cb, ce, db, de);
-    fwd_tile(st.k, st.v, qf, oacc, m_run, l_run, !(entry & kFullBit), iv, a.scale_log2, ro_t, tro_t, g);
+    fwd_tile(cur.k, cur.v, qf, oacc, m_run, l_run, !(entry & kFullBit), iv, a.scale_log2, offs, g);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's loads of tile t+1 have landed
     lds_barrier();
+  };
+  for (int t = 0; t < lw.count; t += 2) {
+    tile(t, ring[0], ring[1]);
+    if (t + 1 >= lw.count) break;
+    tile(t + 1, ring[1], ring[0]);
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
