@@ -127,6 +127,24 @@ struct TileOffsets {
 
 __device__ __forceinline__ const char* byte_ptr(const uint16_t* p) { return reinterpret_cast<const char*>(p); }
 
+// The row-read half of TileOffsets alone, for kernels without register room for the other half.
+struct RowOffsets {
+  uint32_t row[8];
+  __device__ __forceinline__ explicit RowOffsets(int lane) {
+    const int ro = row_operand_off(lane & 31, lane >> 5);
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) row[ds] = static_cast<uint32_t>(ro ^ (ds << 4)) * 2u;
+  }
+};
+
+struct RowOperandR {
+  const uint16_t* tile;
+  const RowOffsets& o;
+  __device__ __forceinline__ uint4 step(int ds) const {
+    return *reinterpret_cast<const uint4*>(byte_ptr(tile) + o.row[ds]);
+  }
+};
+
 // Row-major operand read through TileOffsets.
 struct RowOperandT {
   const uint16_t* tile;
@@ -662,7 +680,8 @@ __device__ __forceinline__ uint32_t interval_bits(int lo, int hi, int base) {
 
 // acc = A x B over the 128-dim reduction: A rows from LDS (all eight k-steps read up front), B
 // from registers.
-__device__ __forceinline__ f32x16 mfma_chain_lds_reg(const RowOperand& ra, const bf16x8 (&b)[8]) {
+template <typename Operand>
+__device__ __forceinline__ f32x16 mfma_chain_lds_reg(const Operand& ra, const bf16x8 (&b)[8]) {
   uint4 x[8];
 #pragma unroll
   for (int ds = 0; ds < 8; ++ds) x[ds] = ra.step(ds);
@@ -692,7 +711,7 @@ __device__ __forceinline__ void mfma_tr_32(f32x16 (&acc)[4], const uint16_t* til
 // A fully visible stage (a full tile with all rows real) skips the visibility words and the mask.
 __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf16x8 (&kf)[8],
                                             f32x16 (&dvacc)[4], float scale_log2, int w, int valid,
-                                            bool all_visible, int key_base, int ro,
+                                            bool all_visible, int key_base, const RowOffsets& ro,
                                             const TrOffsets& tro, int lane) {
   const int g = lane >> 5;
   const int c = lane & 31;
@@ -710,7 +729,7 @@ __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf1
   f32x4 l4[4];
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq) l4[rq] = *reinterpret_cast<const f32x4*>(s.lse2 + rq * 8 + g * 4);
-  f32x16 sacc = mfma_chain_lds_reg(RowOperand{s.q, ro}, kf);  // rows: queries, lane: key
+  f32x16 sacc = mfma_chain_lds_reg(RowOperandR{s.q, ro}, kf);  // rows: queries, lane: key
   if (all_visible) {
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq)
@@ -739,9 +758,9 @@ __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf1
 // dS wave: dP, dS = P (dP - delta) and dK += dS^T Q for one stage.
 __device__ __forceinline__ void dkdv_ds_step(const KvStage& s, const PExchange& px,
                                              const bf16x8 (&vf)[8], f32x16 (&dkacc)[4], int w,
-                                             int ro, const TrOffsets& tro, int lane) {
+                                             const RowOffsets& ro, const TrOffsets& tro, int lane) {
   const int g = lane >> 5;
-  f32x16 dp = mfma_chain_lds_reg(RowOperand{s.dout, ro}, vf);
+  f32x16 dp = mfma_chain_lds_reg(RowOperandR{s.dout, ro}, vf);
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq) {
     const int r0 = rq * 8 + g * 4;
@@ -844,7 +863,7 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   load_row_frag(kvf, p_role ? a.k + ksafe * a.kst + hkv * a.ksh : a.v + ksafe * a.vst + hkv * a.vsh,
                 valid_k, g);
   f32x16 acc[4] = {};
-  const int ro = row_operand_off(c, g);
+  const RowOffsets ro(lane);
   const TrOffsets tro(lane);
 
   // Loads of iteration `it` into a stage. Wave v moves Q and dO rows 4v .. 4v+3 (lane l lands at
@@ -903,9 +922,7 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
                   PExchange& x_prv) {
     const bool ahead = i + 2 < iters;
     if (ahead) issue(i + 2, s_ld);
-    int ro_t = ro;
     TrOffsets tro_t = tro;
-    opaque(ro_t);
     opaque(tro_t.lo);
     opaque(tro_t.hi);
     if constexpr (decltype(role)::value) {
@@ -915,10 +932,10 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
       row_base(i, q0, head, valid);
       const bool full = (static_cast<uint32_t>(__builtin_amdgcn_readlane(my_tile, i / G)) & kFullBit) != 0;
       dkdv_p_step(live ? s_cur : st3, x_cur, kvf, acc, a.scale_log2, w, live ? valid : 0,
-                  live && full && valid == kBwdTileM, static_cast<int>(key0) + w * 32, ro_t, tro_t,
+                  live && full && valid == kBwdTileM, static_cast<int>(key0) + w * 32, ro, tro_t,
                   lane);
     } else {
-      dkdv_ds_step(s_prv, x_prv, kvf, acc, w, ro_t, tro_t, lane);  // trip 0: stage 3 and buffer 1
+      dkdv_ds_step(s_prv, x_prv, kvf, acc, w, ro, tro_t, lane);  // trip 0: stage 3 and buffer 1
     }
     wait_loads(ahead);  // this wave's part of stage i+1 has landed
     lds_barrier();
