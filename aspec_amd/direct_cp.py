@@ -302,11 +302,34 @@ class _DSparkAttention(torch.autograd.Function):
             _lib.ptr(dv), dv.stride(1), dv.stride(2), _lib.ptr(workspace),
             _lib.stream_handle(q.device),
         )
-        for stage, name in ((1, "attn_bwd_prepare"), (2, "attn_bwd_dq"), (4, "attn_bwd_dkdv"),
-                            (8, "attn_bwd_finalize")):
-            with _timing.region(name):
-                _lib.call("aspec_dspark_attn_bwd_stages", stage, *args)
+        # dQ and dK/dV depend only on the prepare stage: dQ runs on a second stream (default
+        # priority) beside dK/dV, so each fills the other's tail of partly occupied CUs.
+        main = torch.cuda.current_stream(q.device)
+        side = _backward_side_stream(q.device)
+        with _timing.region("attn_bwd_prepare"):
+            _lib.call("aspec_dspark_attn_bwd_stages", 1, *args)
+        side.wait_stream(main)
+        with torch.cuda.stream(side), _timing.region("attn_bwd_dq"):
+            _lib.call("aspec_dspark_attn_bwd_stages", 2, *args[:-1], side.cuda_stream)
+        with _timing.region("attn_bwd_dkdv"):
+            _lib.call("aspec_dspark_attn_bwd_stages", 4, *args)
+        with _timing.region("attn_bwd_finalize"):
+            _lib.call("aspec_dspark_attn_bwd_stages", 8, *args)
+        main.wait_stream(side)
         return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None, None, None
+
+
+_side_streams: dict = {}
+
+
+def _backward_side_stream(device) -> torch.cuda.Stream:
+    """One extra stream per device for the attention backward (created once, default priority)."""
+    key = torch.device(device).index
+    stream = _side_streams.get(key)
+    if stream is None:
+        stream = torch.cuda.Stream(device=device)
+        _side_streams[key] = stream
+    return stream
 
 
 def dspark_attention(query: Tensor, key: Tensor, value: Tensor, metadata: DirectCPMetadata,

@@ -26,6 +26,21 @@ def decay_weights(block_size: int, loss_decay_gamma: Optional[float], prediction
     return torch.ones_like(k, dtype=torch.float32)
 
 
+_decay_tables: dict = {}
+
+
+def _decay_table(block_size: int, loss_decay_gamma: Optional[float], prediction_start: int,
+                 device: torch.device) -> torch.Tensor:
+    """The flattened `decay_weights` table, built once per (block size, gamma, start, device): the
+    same torch expression, so the same values, without its half-dozen launches on every call."""
+    key = (block_size, loss_decay_gamma, prediction_start, str(device))
+    table = _decay_tables.get(key)
+    if table is None:
+        table = decay_weights(block_size, loss_decay_gamma, prediction_start, device).reshape(-1).contiguous()
+        _decay_tables[key] = table
+    return table
+
+
 @dataclass
 class DSparkTargets:
     label_index: torch.Tensor    # [B, nb, bs] int64, min(a + 1 + k, S - 1), 0 for dropped blocks
@@ -51,7 +66,7 @@ def dspark_targets(anchor_positions: torch.Tensor, block_keep_mask: torch.Tensor
     if device.type != "cuda":
         raise ValueError("DSpark targets (HIP) need their tensors on the GPU")
     n_blocks = anchor_positions.shape[1]
-    decay = decay_weights(block_size, loss_decay_gamma, prediction_start, device).reshape(-1).contiguous()
+    decay = _decay_table(block_size, loss_decay_gamma, prediction_start, device)
     anchors = anchor_positions.to(torch.long).contiguous()
     keep = block_keep_mask.contiguous()
     if keep.dtype != torch.bool:

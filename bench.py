@@ -12,6 +12,9 @@ One step = one packed 4096-token row through the draft hot path, inputs resident
      backward (HIP);
   before the head: injected-anchor validation, output-block counts and the DSpark targets (labels,
   eval mask, decay weights) from the anchors (HIP).
+The teacher table runs on a second stream while the host performs the step's host-side checks
+(anchor validation, output-block counts, layout check: one device-to-host read each, as in the
+reference) and launches the metadata kernels; the loss waits for it.
 Row-level operations that run once per row outside the step (packing collator, document anchor
 sampler) and the fused Q/K RMSNorm + RoPE of the draft layer (fwd + bwd at the config-2 geometry;
 config 2's step starts from projected Q/K/V) are timed separately and reported with
@@ -147,10 +150,18 @@ def step(x, head_fn):
 
     w = x["w"]
     anchors, keep, pos, docs, adocs = x["meta_tensors"]
-    # The frozen-teacher table depends on neither the anchors nor the draft: queued first, it keeps
-    # the GPU busy while the host waits on the validation and output-block transfers below.
-    with torch.no_grad(), _timing.region("teacher_gemm"):
+    # The frozen-teacher table depends on neither the anchors nor the draft. It runs on a second
+    # stream (default priority) that starts after the previous step's work, so the GPU computes it
+    # while the host waits on the validation, output-block and layout checks below and launches
+    # the metadata kernels; the loss waits for it.
+    main = torch.cuda.current_stream()
+    side = x.setdefault("side_stream", torch.cuda.Stream(device=main.device))
+    side.wait_stream(main)
+    with torch.cuda.stream(side), torch.no_grad(), _timing.region("teacher_gemm"):
         teacher = torch.matmul(x["target_hidden"], x["head"].t())
+        teacher_done = torch.cuda.Event()
+        teacher_done.record()
+    teacher.record_stream(main)
     # the configs inject their anchors (dflash.py:297-306): validated, then the output-block
     # counts of the compacted head (dspark.py:347-352) and the labels / eval mask / decay weights
     # (dspark.py:240-272, 311-315, 325)
@@ -169,6 +180,7 @@ def step(x, head_fn):
     out, _ = direct_cp_attention_from_kv(x["q"], x["k"], x["v"], meta)
     hidden = out.transpose(1, 2).reshape(w.num_queries, w.q_heads * w.head_dim)
     logits = head_fn.apply(hidden, x["head"], x["head_t"])
+    main.wait_event(teacher_done)
     ce, l1 = ce_l1_from_logits(logits, targets.target_ids.reshape(-1), teacher,
                                teacher_indices=targets.teacher_index.reshape(-1))
     wts = targets.weights.reshape(-1)
