@@ -305,21 +305,40 @@ class _DSparkAttention(torch.autograd.Function):
         # dQ and dK/dV depend only on the prepare stage: dQ runs on a second stream (default
         # priority) beside dK/dV, so each fills the other's tail of partly occupied CUs.
         main = torch.cuda.current_stream(q.device)
-        side = _backward_side_stream(q.device)
+        side = _backward_side_stream(q.device) if _overlap_backward else None
         with _timing.region("attn_bwd_prepare"):
             _lib.call("aspec_dspark_attn_bwd_stages", 1, *args)
-        side.wait_stream(main)
-        with torch.cuda.stream(side), _timing.region("attn_bwd_dq"):
-            _lib.call("aspec_dspark_attn_bwd_stages", 2, *args[:-1], side.cuda_stream)
+        if side is not None:
+            side.wait_stream(main)
+            with torch.cuda.stream(side), _timing.region("attn_bwd_dq"):
+                _lib.call("aspec_dspark_attn_bwd_stages", 2, *args[:-1], side.cuda_stream)
+        else:
+            with _timing.region("attn_bwd_dq"):
+                _lib.call("aspec_dspark_attn_bwd_stages", 2, *args)
         with _timing.region("attn_bwd_dkdv"):
             _lib.call("aspec_dspark_attn_bwd_stages", 4, *args)
         with _timing.region("attn_bwd_finalize"):
             _lib.call("aspec_dspark_attn_bwd_stages", 8, *args)
-        main.wait_stream(side)
+        if side is not None:
+            main.wait_stream(side)
         return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None, None, None
 
 
+_overlap_backward = True
 _side_streams: dict = {}
+
+
+def backward_overlap() -> bool:
+    """Whether the attention backward runs dQ beside dK/dV (see set_backward_overlap)."""
+    return _overlap_backward
+
+
+def set_backward_overlap(enabled: bool) -> None:
+    """Run the attention backward's dQ kernel beside dK/dV on a second stream (the default) or
+    after it on the caller's stream. Both do the same work; the serial order gives each kernel the
+    whole GPU, for per-kernel timing and hardware counters."""
+    global _overlap_backward
+    _overlap_backward = bool(enabled)
 
 
 def _backward_side_stream(device) -> torch.cuda.Stream:

@@ -14,7 +14,10 @@ One step = one packed 4096-token row through the draft hot path, inputs resident
   eval mask, decay weights) from the anchors (HIP).
 The teacher table runs on a second stream while the host performs the step's host-side checks
 (anchor validation, output-block counts, layout check: one device-to-host read each, as in the
-reference) and launches the metadata kernels; the loss waits for it.
+reference) and launches the metadata kernels; the loss waits for it. In the attention backward,
+dQ runs beside dK/dV on a second stream. Per-kernel durations ("kernels", "roofline",
+"attention") come from a second pass over the same steps with both overlaps off, so each kernel
+has the GPU to itself; `--serial` runs the timed steps that way too.
 Row-level operations that run once per row outside the step (packing collator, document anchor
 sampler) and the fused Q/K RMSNorm + RoPE of the draft layer (fwd + bwd at the config-2 geometry;
 config 2's step starts from projected Q/K/V) are timed separately and reported with
@@ -55,6 +58,9 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the timed CPU oracle leg")
     p.add_argument("--no-kernel-timing", action="store_true", help="no per-kernel HIP events")
+    p.add_argument("--serial", action="store_true",
+                   help="timed steps without the stream overlaps (each kernel alone on the GPU, as "
+                        "for the rocprofv3 kernel traces and counters)")
     p.add_argument("--no-gemm-tuning", action="store_true",
                    help="library-default GEMM solutions instead of the recorded TunableOp file")
     p.add_argument("--no-layer-step", action="store_true",
@@ -138,7 +144,7 @@ class _Head:
         return HeadProjection
 
 
-def step(x, head_fn):
+def step(x, head_fn, overlap=True):
     import torch
 
     from aspec_amd import _timing
@@ -155,7 +161,7 @@ def step(x, head_fn):
     # while the host waits on the validation, output-block and layout checks below and launches
     # the metadata kernels; the loss waits for it.
     main = torch.cuda.current_stream()
-    side = x.setdefault("side_stream", torch.cuda.Stream(device=main.device))
+    side = x.setdefault("side_stream", torch.cuda.Stream(device=main.device)) if overlap else main
     side.wait_stream(main)
     with torch.cuda.stream(side), torch.no_grad(), _timing.region("teacher_gemm"):
         teacher = torch.matmul(x["target_hidden"], x["head"].t())
@@ -368,12 +374,18 @@ def layer_step(device, steps, warmup):
     elapsed = time.perf_counter() - t0
     if not (torch.isfinite(loss) and torch.isfinite(norm)):
         raise RuntimeError("non-finite loss or gradient norm in the config-5 steps")
+    # per-region durations with each kernel alone on the GPU (attention dQ after dK/dV)
+    from aspec_amd.direct_cp import backward_overlap, set_backward_overlap
+
+    overlap = backward_overlap()
+    set_backward_overlap(False)
     _timing.reset()
     _timing.enable(True)
     for _ in range(min(steps, 5)):
         dspark_layer_step(model, opt, batch)
     torch.cuda.synchronize()
     _timing.enable(False)
+    set_backward_overlap(overlap)
     stats = _timing.summary()
     n = opt.flat.numel()
     adam_bytes = n * 30  # bf16 grads read twice (norm, update), fp32 master/m/v read + written, bf16 param written
@@ -486,21 +498,35 @@ def main():
     head_fn = _Head.make()
     w = x["w"]
 
+    from aspec_amd.direct_cp import set_backward_overlap
+
+    overlap = not args.serial
+    set_backward_overlap(overlap)
     for _ in range(args.warmup):
-        step(x, head_fn)
-    torch.cuda.synchronize()
-    _timing.reset()
-    _timing.enable(not args.no_kernel_timing)
+        step(x, head_fn, overlap)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        loss = step(x, head_fn)
+        loss = step(x, head_fn, overlap)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    _timing.enable(False)
-    kernels = _timing.summary() if not args.no_kernel_timing else {}
     if not torch.isfinite(loss):
         raise RuntimeError("non-finite loss in the timed steps")
+    kernels = {}
+    if not args.no_kernel_timing:
+        # Per-kernel durations with every kernel alone on the GPU: the same steps again with the
+        # two overlaps (teacher table, dQ beside dK/dV) off.
+        set_backward_overlap(False)
+        step(x, head_fn, False)
+        torch.cuda.synchronize()
+        _timing.reset()
+        _timing.enable(True)
+        for _ in range(args.steps):
+            step(x, head_fn, False)
+        torch.cuda.synchronize()
+        _timing.enable(False)
+        kernels = _timing.summary()
+        set_backward_overlap(overlap)
 
     pairs, work = kernel_work(w)
     per_kernel = {}
@@ -545,7 +571,8 @@ def main():
     if all(k in kernels for k in ("attn_fwd", "attn_bwd_prepare", "attn_bwd_dq", "attn_bwd_dkdv")):
         t_fb = sum(kernels[k]["mean_ms"] for k in ("attn_fwd", "attn_bwd_prepare", "attn_bwd_dq", "attn_bwd_dkdv"))
         flops = 14 * w.q_heads * w.head_dim * pairs  # reference accounting: fwd 4 + bwd 10
-        attn = {"fwd_bwd_ms": round(t_fb, 4), "tflops": round(flops / (t_fb * 1e-3) / 1e12, 2),
+        attn = {"fwd_bwd_ms": round(t_fb, 4), "timing": "sum of the kernels' isolated durations",
+                "tflops": round(flops / (t_fb * 1e-3) / 1e12, 2),
                 "frac_mfma": round(flops / (t_fb * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                 "visible_pairs_per_head": pairs, "gflop_fwd_bwd": round(flops / 1e9, 1)}
 
@@ -568,6 +595,8 @@ def main():
                         "(CE + tiled L1, indexed teacher)",
             "context_tokens": w.context_length, "draft_queries": w.num_queries,
             "parallelism": "single GPU, CP=1",
+            "streams": ("one (--serial)" if args.serial else
+                        "two: teacher table and attention dQ on a second stream"),
             "head_gemms": (f"library GEMMs, TunableOp solutions from {gemm_solutions}" if gemm_solutions
                            else "library GEMMs, default solutions"),
         },
