@@ -155,3 +155,39 @@ def test_config2_full_size_properties(gpu):
     dk_sum = k.grad[0].float().sum(1)
     scale_ref = k.grad[0].float().abs().sum(1)
     assert torch.all(dk_sum.abs() <= 0.02 * scale_ref + 0.05)
+
+
+def test_backward_stream_overlap_matches_serial(gpu):
+    """The backward runs dQ beside dK/dV on a second stream by default; the serial order runs the
+    same kernels on one stream. dQ has no atomics: it must agree bit for bit, over repeated calls at
+    the config-2 geometry. dK/dV rows of key tiles split over several units are summed with fp32
+    atomics in arrival order, so they may differ by one bf16 rounding step between any two runs."""
+    from aspec_amd.direct_cp import backward_overlap, set_backward_overlap
+
+    w = W.config2()
+    meta = W.metadata_for(w, gpu)
+    grads = {}
+    try:
+        for overlap in (False, True):
+            set_backward_overlap(overlap)
+            runs = []
+            for seed in (3, 4, 3):
+                (q, k, v), dout, _ = _inputs(w, gpu, seed)
+                out, _ = direct_cp_attention_from_kv(q, k, v, meta)
+                out.backward(dout)
+                runs.append([x.grad.detach().clone() for x in (q, k, v)])
+            torch.cuda.synchronize()
+            grads[overlap] = runs
+    finally:
+        set_backward_overlap(True)
+    assert backward_overlap()
+
+    def one_step_apart(a, b):
+        a, b = a.float(), b.float()
+        bound = 2.0 ** -7 * a.abs() + 2.0 ** -10 * a.abs().max()
+        return bool(torch.all((a - b).abs() <= bound))
+
+    pairs = list(zip(grads[False], grads[True])) + [(grads[True][0], grads[True][2])]
+    for first, second in pairs:
+        assert torch.equal(first[0], second[0])  # dQ
+        assert one_step_apart(first[1], second[1]) and one_step_apart(first[2], second[2])
