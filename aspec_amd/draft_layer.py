@@ -378,7 +378,8 @@ def dspark_layer_step(model, optimizer, batch, *, ce_alpha=0.1, l1_alpha=0.9):
     ce, l1 = ce_l1_from_logits(logits, targets.target_ids.reshape(-1), teacher,
                                teacher_indices=targets.teacher_index.reshape(-1))
     w = targets.weights.reshape(-1)
-    loss = (ce_alpha * (ce * w).sum() + l1_alpha * (l1 * w).sum()) / w.sum().clamp(min=1e-6)
+    # (a_ce sum(w ce) + a_l1 sum(w l1)) / sum(w) with one dot product (fewer launches)
+    loss = torch.dot(torch.add(ce * ce_alpha, l1, alpha=l1_alpha), w) / w.sum().clamp(min=1e-6)
     loss.backward()
     norm = optimizer.step()
     return loss.detach(), norm

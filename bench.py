@@ -190,7 +190,8 @@ def step(x, head_fn, overlap=True):
     ce, l1 = ce_l1_from_logits(logits, targets.target_ids.reshape(-1), teacher,
                                teacher_indices=targets.teacher_index.reshape(-1))
     wts = targets.weights.reshape(-1)
-    loss = (CE_ALPHA * (ce * wts).sum() + L1_ALPHA * (l1 * wts).sum()) / wts.sum().clamp(min=1e-6)
+    # (0.1 sum(w ce) + 0.9 sum(w l1)) / sum(w), as one add and one dot product (fewer launches)
+    loss = torch.dot(torch.add(l1, ce, alpha=CE_ALPHA / L1_ALPHA), wts) * (L1_ALPHA / wts.sum().clamp(min=1e-6))
     loss.backward()
     return loss
 
