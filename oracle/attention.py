@@ -71,10 +71,12 @@ def attention(q, k, v, visible, scale, *, dout=None, dlse=None, dtype=torch.floa
 
 def attention_row_loop(q, k, v, visible, scale, head, row):
     """One output row by an explicit float64 loop over visible keys (independent restatement
-    used to pin `attention`): returns (out [D], lse)."""
+    used to pin `attention`): returns (out [D], lse). `visible` is the dense [Nq, K] mask or just
+    this row's [K] mask."""
     group = q.shape[0] // k.shape[0]
     kv = head // group
-    keys = np.nonzero(np.asarray(visible)[row])[0]
+    vis = np.asarray(visible)
+    keys = np.nonzero(vis if vis.ndim == 1 else vis[row])[0]
     if keys.size == 0:
         return np.zeros(v.shape[-1]), MASK_VALUE
     qv = q[head, row].double().numpy()

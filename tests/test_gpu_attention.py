@@ -125,11 +125,15 @@ def test_no_active_queries_gives_zero_outputs_and_gradients(gpu):
     assert not q.grad.any() and not k.grad.any() and not v.grad.any()
 
 
-def test_config2_full_size_properties(gpu):
-    """Config 2 at full size: sampled rows against the float64 row loop, plus size-independent
-    identities of the backward: sum_k dV[k] = sum over the GQA group of sum_q dO[q] (rows of P sum
-    to 1) and sum_k dK[k] = 0 (rows of dS sum to 0 when dLSE = 0)."""
-    w = W.config2()
+@pytest.mark.parametrize("make", [W.config2, lambda: W.config3(0, 0), lambda: W.config3(0, 1), W.config4],
+                         ids=["config2", "config3_bin0", "config3_bin1", "config4"])
+def test_full_size_properties(gpu, make):
+    """BASELINE configs 2-4 at full size (config 4: 32K tokens, 2048 anchors, GQA 40/8, a group of
+    five): sampled rows against the float64 row loop, plus size-independent identities of the
+    backward: sum_k dV[k] = sum over the GQA group of sum_q dO[q] (rows of P sum to 1, every row
+    sees at least its own block) and sum_k dK[k] = 0 (rows of dS sum to 0 when dLSE = 0)."""
+    w = make()
+    print(f"{w.name}: {w.num_queries} queries, {w.num_keys} keys, heads {w.q_heads}/{w.kv_heads}", flush=True)
     (q, k, v), dout, _ = _inputs(w, gpu, 5)
     meta = W.metadata_for(w, gpu)
     out, lse = direct_cp_attention_from_kv(q, k, v, meta)
@@ -141,11 +145,9 @@ def test_config2_full_size_properties(gpu):
     rows = rng.choice(w.num_queries, 12, replace=False)
     qc, kc, vc = (x.detach()[0].float().cpu() for x in (q, k, v))
     vis_rows = M.endpoints_to_dense(ends[:, rows], w.num_keys)
-    for head in (0, 13, 31):
+    for head in (0, 13, w.q_heads - 1):
         for i, r in enumerate(rows):
-            vis = np.zeros((w.num_queries, w.num_keys), bool) if i == 0 else vis
-            vis[r] = vis_rows[i]
-            o_ref, l_ref = A.attention_row_loop(qc, kc, vc, vis, w.head_dim ** -0.5, head, r)
+            o_ref, l_ref = A.attention_row_loop(qc, kc, vc, vis_rows[i], w.head_dim ** -0.5, head, r)
             np.testing.assert_allclose(out[0, head, r].detach().float().cpu().numpy(), o_ref, atol=0.025, rtol=0.025)
             assert abs(float(lse[0, head, r].detach()) - l_ref) < 0.025
     group = w.q_heads // w.kv_heads
