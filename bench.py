@@ -22,7 +22,9 @@ Row-level operations that run once per row outside the step (packing collator, d
 sampler) and the fused Q/K RMSNorm + RoPE of the draft layer (fwd + bwd at the config-2 geometry;
 config 2's step starts from projected Q/K/V) are timed separately and reported with
 "outside_step": true.
-After the main measurement the full one-layer DSpark training step of BASELINE config 5 (forward,
+After the main measurement attention forward + backward alone is timed at BASELINE configs 3 (the
+two ragged 32K bins) and 4 (32K document, GQA 40/8) under "attention_configs" (skip with
+--no-attention-configs), and the full one-layer DSpark training step of BASELINE config 5 (forward,
 loss, backward and the fused AdamW) is timed on its own and reported under "config5_layer_step"
 (skip with --no-layer-step).
 Metric: input context tokens per second (4096 per step / wall time), as the reference's draft-only
@@ -58,6 +60,8 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the timed CPU oracle leg")
     p.add_argument("--no-kernel-timing", action="store_true", help="no per-kernel HIP events")
+    p.add_argument("--no-attention-configs", action="store_true",
+                   help="skip the attention-only timings at configs 3 and 4")
     p.add_argument("--serial", action="store_true",
                    help="timed steps without the stream overlaps (each kernel alone on the GPU, as "
                         "for the rocprofv3 kernel traces and counters)")
@@ -196,13 +200,87 @@ def step(x, head_fn, overlap=True):
     return loss
 
 
-def kernel_work(w):
-    """Algorithmic work per launch of each timed region (FLOPs for MFMA-bound, bytes for HBM-bound)."""
-    from oracle import metadata as M
+def visible_pairs(w, device):
+    """Visible (query, key) pairs per head of a workload, from the HIP interval endpoints
+    (context [cb, ce) and draft [db, de) per row; the FLOP accounting of
+    tools/performance/bench_dspark_b7_attention.py:173-193)."""
+    import torch
 
-    ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
-                       w.block_size, w.sequence_length)
-    pairs = M.visible_pairs(ends)
+    from aspec_amd import workloads as W
+    from aspec_amd.direct_cp import thd_row_metadata
+
+    e = thd_row_metadata(W.metadata_for(w, device), device).endpoints.to(torch.int64)
+    return int(((e[2] - e[1]).sum() + (e[4] - e[3]).sum()).item())
+
+
+def attention_configs(device, reps):
+    """Attention forward + backward alone at BASELINE configs 3 (both ragged 32K bins of 64
+    log-normal documents) and 4 (one 32K document, 2048 anchors, GQA 40/8): wall time per
+    fwd + bwd with the two-stream backward, and the kernels' isolated durations."""
+    import torch
+
+    from aspec_amd import _timing
+    from aspec_amd import workloads as W
+    from aspec_amd.direct_cp import backward_overlap, direct_cp_attention_from_kv, set_backward_overlap
+
+    out = {}
+    overlap = backward_overlap()
+    for w in (W.config3(0, 0), W.config3(0, 1), W.config4()):
+        g = torch.Generator(device=device).manual_seed(0)
+
+        def rows(n, h, scale):
+            x = torch.randn(1, n, h, w.head_dim, device=device, generator=g) * scale
+            return x.to(torch.bfloat16).transpose(1, 2)
+
+        q, k, v = (rows(w.num_queries, w.q_heads, 0.5).requires_grad_(),
+                   rows(w.num_keys, w.kv_heads, 0.5).requires_grad_(),
+                   rows(w.num_keys, w.kv_heads, 0.5).requires_grad_())
+        dout = rows(w.num_queries, w.q_heads, 1.0)
+        meta = W.metadata_for(w, device)
+
+        def once():
+            for t in (q, k, v):
+                t.grad = None
+            o, _ = direct_cp_attention_from_kv(q, k, v, meta)
+            o.backward(dout)
+
+        for _ in range(2):
+            once()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            once()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / reps
+        set_backward_overlap(False)
+        _timing.reset()
+        _timing.enable(True)
+        for _ in range(reps):
+            once()
+        torch.cuda.synchronize()
+        _timing.enable(False)
+        set_backward_overlap(overlap)
+        st = _timing.summary()
+        kernels = ("attn_fwd", "attn_bwd_prepare", "attn_bwd_dq", "attn_bwd_dkdv", "attn_bwd_finalize")
+        iso = sum(st[n]["mean_ms"] for n in kernels)
+        pairs = visible_pairs(w, device)
+        flops = 14 * w.q_heads * w.head_dim * pairs  # reference accounting: fwd 4 + bwd 10
+        out[w.name] = {
+            "documents": len(w.lengths), "context_tokens": w.context_length, "queries": w.num_queries,
+            "keys": w.num_keys, "heads": f"{w.q_heads}/{w.kv_heads}", "visible_pairs_per_head": pairs,
+            "gflop_fwd_bwd": round(flops / 1e9, 1), "wall_ms": round(wall * 1e3, 4),
+            "context_tokens_per_s": round(w.context_length / wall, 1),
+            "kernels_ms": {n: round(st[n]["mean_ms"], 4) for n in kernels},
+            "isolated_fwd_bwd_ms": round(iso, 4),
+            "tflops": round(flops / (iso * 1e-3) / 1e12, 2),
+            "frac_mfma": round(flops / (iso * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+        del q, k, v, dout, meta
+    return out
+
+
+def kernel_work(w, device):
+    """Algorithmic work per launch of each timed region (FLOPs for MFMA-bound, bytes for HBM-bound)."""
+    pairs = visible_pairs(w, device)
     hd = w.q_heads * w.head_dim
     rows, ctx = w.num_queries, w.context_length
     return pairs, {
@@ -529,7 +607,7 @@ def main():
         kernels = _timing.summary()
         set_backward_overlap(overlap)
 
-    pairs, work = kernel_work(w)
+    pairs, work = kernel_work(w, device)
     per_kernel = {}
     for name, stats in kernels.items():
         bound, amount = work.get(name, (None, None))
@@ -607,6 +685,8 @@ def main():
         "kernels": per_kernel,
         "cpu_baseline": None,
     }
+    if not args.no_attention_configs:
+        result["attention_configs"] = attention_configs(device, max(3, args.steps // 4))
     if not args.no_layer_step:
         result["config5_layer_step"] = layer_step(device, max(3, args.steps // 2), 2)
     if not args.no_cpu_baseline:
