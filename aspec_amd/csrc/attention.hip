@@ -364,7 +364,7 @@ __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb][r] = iv.visible(kb * 32 + c_row(r, g)) ? s[kb][r] : -INFINITY;
+      for (int r = 0; r < 16; ++r) s[kb][r] = masked_score(s[kb][r], iv.word(kb, g), r);
   }
   float tile_max = -INFINITY;
 #pragma unroll
@@ -548,7 +548,7 @@ __device__ __forceinline__ void dq_tile(const uint16_t* sk, const uint16_t* sv,
     read_tr_first(kcur, sk + kb * 32 * kRowLd, tro);
     if (partial) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = iv.visible(kb * 32 + c_row(r, g)) ? s[r] : -INFINITY;
+      for (int r = 0; r < 16; ++r) s[r] = masked_score(s[r], iv.word(kb, g), r);
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -670,13 +670,6 @@ static_assert(offsetof(KvStage, ends) == offsetof(KvStage, delta) + 4 * kBwdTile
 struct PExchange {
   f32x4 p[kKvWaves][4][kWave];
 };
-
-// Bits [lo, hi) of the 32-key word starting at `base`.
-__device__ __forceinline__ uint32_t interval_bits(int lo, int hi, int base) {
-  const int a = min(max(lo - base, 0), 32);
-  const int e = min(max(hi - base, 0), 32);
-  return e > a ? static_cast<uint32_t>((1ull << e) - (1ull << a)) : 0u;
-}
 
 // acc = A x B over the 128-dim reduction: A rows from LDS (all eight k-steps read up front), B
 // from registers.

@@ -127,6 +127,13 @@ __device__ __forceinline__ bool interval_visible(int key, int cb, int ce, int db
   return in_ctx | in_draft;
 }
 
+// Bits [lo, hi) of the 32-key word starting at `base`.
+__device__ __forceinline__ uint32_t interval_bits(int lo, int hi, int base) {
+  const int a = min(max(lo - base, 0), 32);
+  const int e = min(max(hi - base, 0), 32);
+  return e > a ? static_cast<uint32_t>((1ull << e) - (1ull << a)) : 0u;
+}
+
 // Row-interval form used per tile: offsets relative to the tile's first key, so the per-element
 // test is two compares against values held in registers.
 struct RowIntervals {
@@ -141,6 +148,17 @@ struct RowIntervals {
     return (static_cast<uint32_t>(off - c0) < static_cast<uint32_t>(cl)) |
            (static_cast<uint32_t>(off - d0) < static_cast<uint32_t>(dl));
   }
+  // Visibility of keys 32*kb .. 32*kb+31 of the tile as one word, shifted right by 4*g so that
+  // bit (r/4)*8 + r%4 is the key of C register r for lane group g (c_row(r, g) = that + 4*g).
+  __device__ __forceinline__ uint32_t word(int kb, int g) const {
+    return (interval_bits(c0, c0 + cl, kb * 32) | interval_bits(d0, d0 + dl, kb * 32)) >> (4 * g);
+  }
 };
+
+// The score of C register r, or -inf when its key is not visible (`w` from RowIntervals::word).
+__device__ __forceinline__ float masked_score(float s, uint32_t w, int r) {
+  const int keep = __builtin_amdgcn_sbfe(static_cast<int>(w), (r >> 2) * 8 + (r & 3), 1);  // 0 or -1
+  return __int_as_float((__float_as_int(s) & keep) | (~keep & static_cast<int>(0xff800000u)));
+}
 
 }  // namespace aspec
