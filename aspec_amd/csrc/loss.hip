@@ -139,6 +139,16 @@ constexpr int kWalkWaves = kWalkThreads / 64;
 
 // Per-thread max and exp2 values of NV chunks of eight bf16 logits (chunk j of thread t holds
 // row elements (j * kWalkThreads + t) * 8 .. +7; value i of `e` is element i % 8 of chunk i / 8).
+// max(a, b, c) as the hardware computes it (a NaN operand is skipped, like fmaxf). Through fmaxf
+// the compiler first quiets every operand with a max of the value with itself, which more than
+// doubles the cost of the row maximum; a NaN logit still reaches the row sum (and so the loss)
+// through its exp.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 template <int NV>
 __device__ __forceinline__ void chunk_exps(const uint4 (&v)[NV], float (&e)[NV * 8], float& m,
                                            float& sum) {
@@ -147,7 +157,7 @@ __device__ __forceinline__ void chunk_exps(const uint4 (&v)[NV], float (&e)[NV *
   for (int j = 0; j < NV; ++j) {
     const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-    for (int k = 0; k < 4; ++k) m = fmaxf(m, fmaxf(lo_bf(w[k]), hi_bf(w[k])));
+    for (int k = 0; k < 4; ++k) m = max3_raw(m, lo_bf(w[k]), hi_bf(w[k]));
   }
   const float nm = m == -INFINITY ? 0.f : neg_scaled_max(m);
   sum = 0.f;
