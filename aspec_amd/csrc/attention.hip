@@ -653,6 +653,7 @@ struct Role {
 };
 
 constexpr int kDkdvWaves = 2 * kKvWaves;
+static_assert(kBwdChunk <= kWave, "a unit's query tiles are held one per lane");
 constexpr int kDkdvStages = 4;
 
 struct KvStage {
@@ -844,7 +845,7 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   const int iters = max(0, last - first) * G;
   const int32_t* list = a.plan.b_list + n * a.plan.nmb;
   const int64_t key0 = n * kBwdTileN;
-  // The unit's (at most 32) query tiles, one per lane, read with readlane in the loop: no memory
+  // The unit's (at most kBwdChunk = 64) query tiles, one per lane, read with readlane in the loop: no memory
   // access there besides the stage loads.
   const int my_tile = lane < last - first ? list[first + lane] : 0;  // query tile | kFullBit
 

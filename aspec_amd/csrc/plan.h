@@ -13,7 +13,7 @@ constexpr int kFwdTileN = 64;
 constexpr int kBwdTileM = 32;
 constexpr int kBwdTileN = 128;
 // dK/dV work units cover at most this many query tiles of one key tile.
-constexpr int kBwdChunk = 32;
+constexpr int kBwdChunk = 64;
 // List entries carry the tile index in the low bits and "full tile" in bit 31.
 constexpr uint32_t kFullBit = 0x80000000u;
 

@@ -47,6 +47,7 @@ __global__ void __launch_bounds__(kWave) plan_cols_kernel(PlanView p) {
 
 // One workgroup: counting sort of the (key tile, chunk) units by chunk length, longest first.
 constexpr int kUnitThreads = 1024;
+static_assert(kBwdChunk < kUnitThreads, "one thread per histogram bin");
 
 __global__ void __launch_bounds__(kUnitThreads) plan_units_kernel(PlanView p) {
   __shared__ int32_t hist[kBwdChunk + 1];
