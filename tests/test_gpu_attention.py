@@ -100,8 +100,11 @@ def test_windows_and_causal(gpu, masks):
     _check(w, gpu, seed=11, masks=masks)
 
 
-def test_config1_fwd_bwd(gpu):
-    _check(W.config1(0), gpu, seed=0)
+@pytest.mark.parametrize("seed", [0, 3, 7, 11])
+def test_config1_fwd_bwd(gpu, seed):
+    """BASELINE config 1 (4 documents, lengths seeded in [256, 1024]) for several seeds: each seed
+    gives a different ragged layout."""
+    _check(W.config1(seed), gpu, seed=seed)
 
 
 def test_config1_head_major_inputs_without_dlse(gpu):
