@@ -21,7 +21,6 @@ constexpr int kTM = kFwdTileM;          // query rows per wave (one per lane col
 constexpr int kTN = kFwdTileN;          // keys per tile
 constexpr int kMaxGroup = 8;
 constexpr int kKvWaves = kBwdTileN / 32;
-constexpr int kUnitChunkBits = 12;
 // Online softmax keeps a stale row maximum until a tile raises it by more than 2^8: exp2 of the
 // shifted scores stays <= 256 (exact in fp32, fine in bf16) and O is rescaled only then.
 constexpr float kRescaleThreshold = 8.f;

@@ -16,6 +16,8 @@ constexpr int kBwdTileN = 128;
 constexpr int kBwdChunk = 64;
 // List entries carry the tile index in the low bits and "full tile" in bit 31.
 constexpr uint32_t kFullBit = 0x80000000u;
+// dK/dV work units are packed as (key tile << kUnitChunkBits) | chunk.
+constexpr int kUnitChunkBits = 12;
 
 struct PlanView {
   int64_t nmf, nnf, nmb, nnb, max_units;
@@ -26,7 +28,7 @@ struct PlanView {
   int32_t* b_cnt;     // [nnb] visible query tiles per key tile
   int32_t* b_list;    // [nnb][nmb] descending query tiles | kFullBit
   int32_t* b_chunks;  // [nnb] work units of each key tile (>= 1)
-  int32_t* b_units;   // [max_units] (key tile << 16 | chunk), longest first
+  int32_t* b_units;   // [max_units] (key tile << kUnitChunkBits | chunk), longest first
   int32_t* b_nunits;  // [1]
   size_t bytes;
 };

@@ -5,8 +5,6 @@
 namespace aspec {
 namespace {
 
-constexpr int kUnitChunkBits = 12;
-
 // One wave per query tile: ascending list of visible key tiles.
 __global__ void __launch_bounds__(kWave) plan_rows_kernel(PlanView p) {
   const int64_t m = blockIdx.x;

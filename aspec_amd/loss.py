@@ -17,6 +17,32 @@ from aspec_amd import _lib, _timing
 STATS = 8
 
 
+class IndexCheck:
+    """Fail-closed check of the indices a loss forward consumed (the reference device-asserts on an
+    out-of-range teacher index, tiled_l1.py:41-42, and torch's cross-entropy on a bad target).
+
+    The forward ORs bit 1 (teacher index) / bit 2 (target) into a device flag and writes NaN rows.
+    The flag is copied into pinned host memory behind an event on the launch stream, so reading it
+    later costs no stall: the backward reads it before it launches, and a forward that no backward
+    will follow reads it at once. Either raises ValueError."""
+
+    def __init__(self, flags: torch.Tensor):
+        self.host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        self.host.copy_(flags, non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record(torch.cuda.current_stream(flags.device))
+
+    def raise_if_bad(self) -> None:
+        self.event.synchronize()
+        bad = int(self.host[0])
+        if bad & 1:
+            raise ValueError("teacher index out of range: every target index must address a row "
+                             "of the teacher table")
+        if bad & 2:
+            raise ValueError("cross-entropy target out of range: targets must lie in [0, vocab) "
+                             "or equal ignore_index")
+
+
 def _check_logits(logits):
     if not logits.is_cuda:
         raise ValueError("loss kernels require CUDA logits")
@@ -47,7 +73,9 @@ class _CeL1(torch.autograd.Function):
         ctx.save_for_backward(logits, targets, teacher, indices, stats)
         ctx.ignore_index = ignore_index
         ctx.trows = trows
-        ctx.flags = flags
+        ctx.index_check = IndexCheck(flags)
+        if not ctx.needs_input_grad[0]:
+            ctx.index_check.raise_if_bad()
         ctx.set_materialize_grads(False)
         if l1 is None:
             l1 = torch.zeros_like(ce)
@@ -59,6 +87,7 @@ class _CeL1(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_ce, grad_l1, grad_argmax=None):
+        ctx.index_check.raise_if_bad()
         logits, targets, teacher, indices, stats = ctx.saved_tensors
         vocab = logits.shape[-1]
         rows = logits.numel() // vocab

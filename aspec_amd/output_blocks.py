@@ -98,14 +98,3 @@ def restore_blocks(value: torch.Tensor, indices: torch.Tensor, original_width: i
         1, index.expand_as(value), value
     )
 
-
-def empty_prediction_terms(hidden: torch.Tensor, heads) -> tuple[torch.Tensor, ...]:
-    """Avoid projections but retain reduction hooks (output_blocks.py:101-112)."""
-    zero = hidden.float().sum() * 0
-    for head in heads:
-        if head is not None:
-            for parameter in head.parameters():
-                if parameter.requires_grad:
-                    zero = zero + parameter.reshape(-1)[:0].sum().float()
-    positions = hidden.new_zeros(hidden.shape[-2], dtype=torch.float32)
-    return zero, zero, zero, positions, positions.clone()

@@ -5,7 +5,8 @@ sum_v |softmax(x)_v - softmax(y)_v| in fp32 from bf16 logits, a frozen teacher (
 int64-indexed teacher table), eight fp32 statistics per row kept for the backward (and for an
 optional checkpoint replay cache), backward p * (sign - E_p[sign]) in the cancellation-free form.
 The HIP forward reads each logit row once; the backward reads x and y once and writes dx once.
-Out-of-range teacher indices produce NaN rows and set a device flag (no host synchronisation).
+Out-of-range teacher indices fail closed: the forward writes NaN rows and a device flag, and the
+backward (or, when no backward follows, the forward itself) raises ValueError.
 """
 
 from __future__ import annotations
@@ -14,6 +15,7 @@ import torch
 from torch.autograd.function import once_differentiable
 
 from aspec_amd import _lib
+from aspec_amd.loss import IndexCheck
 
 STATS = 8
 
@@ -41,7 +43,9 @@ class _TiledL1(torch.autograd.Function):
                 raise ValueError("L1 checkpoint statistics belong to a different head chunk")
         else:
             stats, loss, flags = _forward_stats(logits, target, indices, rows, vocab)
-            ctx.flags = flags
+            ctx.index_check = IndexCheck(flags)
+            if not ctx.needs_input_grad[0]:
+                ctx.index_check.raise_if_bad()
             if replay_cache is not None:
                 replay_cache["statistics"] = stats, loss.detach()
                 replay_cache["vocab"] = vocab
@@ -51,6 +55,9 @@ class _TiledL1(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, gradient):
+        check = getattr(ctx, "index_check", None)
+        if check is not None:
+            check.raise_if_bad()
         logits, target, stats, indices = ctx.saved_tensors
         vocab = logits.shape[-1]
         rows = logits.numel() // vocab

@@ -132,7 +132,10 @@ int aspec_dspark_attn_bwd_workspace_bytes(int64_t num_queries, int64_t num_keys,
  * DSpark attention backward: dQ, dK, dV (bf16) from dO (bf16) and an optional dLSE (fp32 [Hq][Nq],
  * NULL = zero). Replaces FA4's block-sparse backward and `_InternalGQA.backward`
  * (aspec/models/ops/cudnn_gqa_backward.py:128-342): the q heads of one KV group are reduced
- * inside the kernel, so dK/dV are written once, without atomics. Same layout rules as the forward.
+ * inside the kernel. dQ is written once per row (deterministic). A key tile whose query list fits
+ * one work unit writes its dK/dV rows once (deterministic); a key tile split over several units
+ * (long context prefixes) sums its fp32 partials with atomics in arrival order, so those bf16 rows
+ * may differ by one rounding step between runs. Same layout rules as the forward.
  */
 int aspec_dspark_attn_bwd(const void* q, int64_t q_stride_token, int64_t q_stride_head,
                           const void* k, int64_t k_stride_token, int64_t k_stride_head,
@@ -179,7 +182,8 @@ int aspec_loss_stats_floats(void);
  *   ce_out[r] = logsumexp(x_r) - x_r[targets[r]]            (0 where targets[r] == ignore_index)
  * Either output may be NULL (then the teacher / targets may be NULL too). stats [rows][8] fp32 is
  * required and feeds the backward. Out-of-range teacher indices / targets set bits 1 / 2 of
- * *status_flags (caller-zeroed) and produce NaN rows.
+ * *status_flags (caller-zeroed) and produce NaN rows; the caller must read the flag and fail
+ * closed (the Python wrappers raise ValueError, as the reference device-asserts).
  * Replaces `tiled_l1_from_logits` forward (aspec/models/ops/tiled_l1.py:130-209) and
  * `F.cross_entropy(reduction="none")` as called at aspec/models/dspark.py:568-570.
  */

@@ -94,11 +94,35 @@ def test_indexed_teacher_equals_gathered_teacher_bitwise(gpu):
     assert torch.equal(a.grad, b.grad)
 
 
-def test_out_of_range_teacher_index_gives_nan_row(gpu):
+def test_out_of_range_teacher_index_fails_closed(gpu):
+    """The reference device-asserts on an index outside the teacher table (tiled_l1.py:41-42).
+    Here the forward writes a NaN row and the backward raises; a forward that no backward follows
+    raises at once."""
     table = torch.randn(3, 4096, device=gpu, dtype=torch.bfloat16)
     draft = torch.randn(2, 4096, device=gpu, dtype=torch.bfloat16)
-    loss = tiled_l1_from_logits(draft, table, target_indices=torch.tensor([1, 9], device=gpu))
+    bad = torch.tensor([1, 9], device=gpu)
+    with pytest.raises(ValueError, match="teacher index out of range"):
+        tiled_l1_from_logits(draft, table, target_indices=bad)
+    x = draft.clone().requires_grad_()
+    loss = tiled_l1_from_logits(x, table, target_indices=bad)
     assert torch.isfinite(loss[0]) and torch.isnan(loss[1])
+    with pytest.raises(ValueError, match="teacher index out of range"):
+        loss.sum().backward()
+    # the fused CE + L1 entry point fails closed the same way, for teachers and for targets
+    targets = torch.tensor([0, 5], device=gpu)
+    with pytest.raises(ValueError, match="teacher index out of range"):
+        ce_l1_from_logits(draft, targets, table, teacher_indices=bad)
+    with pytest.raises(ValueError, match="target out of range"):
+        ce_l1_from_logits(draft, torch.tensor([0, 4096], device=gpu), table,
+                          teacher_indices=torch.tensor([0, 1], device=gpu))
+    x = draft.clone().requires_grad_()
+    ce, l1 = ce_l1_from_logits(x, torch.tensor([-5, 3], device=gpu))
+    assert torch.isnan(ce[0]) and torch.isfinite(ce[1])
+    with pytest.raises(ValueError, match="target out of range"):
+        ce.sum().backward()
+    # in-range indices pass and leave nothing pending
+    ok = tiled_l1_from_logits(draft, table, target_indices=torch.tensor([2, 0], device=gpu))
+    assert torch.isfinite(ok).all()
 
 
 def test_tiled_l1_rejects_invalid_kernel_inputs(gpu):
