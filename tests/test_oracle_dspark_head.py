@@ -110,3 +110,44 @@ def test_prediction_terms_compose_the_reference_terms():
     assert out[1] == pytest.approx((l1 * weights).sum(), rel=1e-12)
     np.testing.assert_allclose(out[3], (ce * mask).sum((0, 1)), rtol=1e-12)
     assert out[5].shape == (2, K + 1)
+
+
+def test_prediction_terms_conf_num_and_position_correct_hand_computed():
+    """One batch, two blocks of three positions, V = H = 3, W = I (logits = h). By hand:
+    - argmax of the rows: block 0 -> [0, 1, 2], block 1 -> [2, 2, 0]; targets [0, 0, 2] and
+      [2, 1, 0]; eval mask [1, 1, 1] and [1, 1, 0], so the correct-and-evaluated counts per
+      position are [1 + 1, 0 + 0, 1 + 0] = [2, 0, 1];
+    - the teacher equals the draft on positions 0 and 1 (L1 = 0, accept = 1) and is a far one-hot
+      elsewhere on position 2 (L1 = 2 up to e^-60, accept = 0);
+    - the confidence head reads [h | w1[prev]] with weight (0, 0, 0 | 1, 0) and bias 0.5, and
+      w1[t] = (t, 0), so its logit is prev + 0.5; BCE(x, 1) = log(1 + e^-x), BCE(x, 0) =
+      log(1 + e^x); conf_num = sum of weights x BCE."""
+    big = 60.0
+    h = np.array([[[[big, 0, 0], [0, big, 0], [0, 0, big]],
+                   [[0, 1, big], [0, 0, big], [big, 0, 0]]]], np.float64)
+    teacher = h.copy()
+    teacher[0, 0, 2] = [big, 0, 0]
+    teacher[0, 1, 2] = [0, big, 0]
+    w = np.eye(3)
+    tgt = np.array([[[0, 0, 2], [2, 1, 0]]])
+    prev = np.array([[[1, 2, 0], [0, 1, 2]]])
+    mask = np.array([[[1.0, 1.0, 1.0], [1.0, 1.0, 0.0]]])
+    weights = mask * np.array([1.0, 0.5, 0.25])
+    w1 = np.array([[0.0, 0.0], [1.0, 0.0], [2.0, 0.0]])
+    w2 = np.zeros((3, 2))
+    cw = np.array([0.0, 0.0, 0.0, 1.0, 0.0])
+    out = odh.prediction_terms(h, tgt, prev, w, teacher, mask, weights, w1=w1, w2=w2, conf_w=cw,
+                               conf_b=0.5, conf_alpha=1.0)
+    np.testing.assert_array_equal(out[4], [2.0, 0.0, 1.0])
+    x = prev + 0.5
+    accept = np.array([[[1, 1, 0], [1, 1, 0]]], np.float64)
+    bce = np.where(accept == 1, np.log1p(np.exp(-x)), np.log1p(np.exp(x)))
+    assert out[2] == pytest.approx(float((bce * weights).sum()), rel=1e-12, abs=1e-12)
+    # without the Markov features the logit is the bias alone
+    out_plain = odh.prediction_terms(h, tgt, prev, w, teacher, mask, weights, w1=w1, w2=w2,
+                                     conf_w=cw[:3], conf_b=0.5, conf_alpha=1.0, conf_with_markov=False)
+    bce0 = np.where(accept == 1, math.log1p(math.exp(-0.5)), math.log1p(math.exp(0.5)))
+    assert out_plain[2] == pytest.approx(float((bce0 * weights).sum()), rel=1e-12)
+    # the acceptance totals see alpha = accept * mask: per position [2, 2, 0] and tau = 1 + 1 + 1
+    # for both blocks (the cumulative product stops at position 2)
+    np.testing.assert_allclose(out[5], [[2.0, 2.0, 0.0, 6.0], [2.0, 2.0, 1.0, 2.0]], atol=1e-12)

@@ -114,3 +114,96 @@ def test_layer_forward_is_differentiable_and_row_local():
     # keys of the context are masked: the context projection receives no gradient through attention
     assert float(P["context_proj"].grad.abs().max()) == 0.0
     assert float(P["q_proj"].grad.abs().max()) > 0.0
+
+
+def _layer_params(H, D, hq, hkv, F, V, *, scale=0.1, seed=5):
+    r = _rng(seed)
+    return {
+        "embed_tokens": r.standard_normal((V, H)), "context_proj": r.standard_normal((H, 3 * H)) * scale,
+        "context_norm": np.ones(H), "input_layernorm": np.ones(H), "q_proj": r.standard_normal((hq * D, H)),
+        "k_proj": r.standard_normal((hkv * D, H)), "v_proj": r.standard_normal((hkv * D, H)),
+        "q_norm": np.ones(D), "k_norm": np.ones(D), "o_proj": r.standard_normal((H, hq * D)) * scale,
+        "post_attention_layernorm": np.ones(H), "gate_up_proj": r.standard_normal((2 * F, H)) * scale,
+        "down_proj": r.standard_normal((H, F)) * scale, "final_norm": np.ones(H)}
+
+
+def _run_layer(params, th, ids, T, nq, vis, D, eps):
+    cos, sin = np.ones((64, D)), np.zeros((64, D))
+    out = ol.layer_forward(params, th, ids, np.arange(T), np.arange(nq), vis, cos, sin, eps)
+    return out.detach().numpy()
+
+
+def test_layer_forward_without_attention_and_mlp_is_final_norm_of_the_embedding():
+    """o_proj = 0 and down_proj = 0 remove both sublayers: both residual adds leave the embedding
+    row as is, so the output is final_norm(embed[id]). Constant embedding rows c give sign(c) * w
+    (RMSNorm of a constant row). A missing residual gives 0, a missing final norm gives c."""
+    H, D, hq, hkv, F, T, nq, V = 8, 4, 2, 1, 16, 5, 3, 6
+    P = _layer_params(H, D, hq, hkv, F, V)
+    P["o_proj"][:] = 0.0
+    P["down_proj"][:] = 0.0
+    consts = np.array([3.0, -0.5, 2.0, -7.0, 1.5, 0.25])
+    P["embed_tokens"] = np.repeat(consts[:, None], H, axis=1)
+    w = np.linspace(-2.0, 2.0, H)
+    P["final_norm"] = w
+    vis = _rng(6).random((nq, T + nq)) < 0.5
+    vis[:, T:] = True
+    ids = [3, 1, 4]
+    out = _run_layer(P, _rng(7).standard_normal((1, T, 3 * H)), ids, T, nq, vis, D, 1e-12)
+    np.testing.assert_allclose(out, np.sign(consts[ids])[:, None] * w[None], rtol=1e-9, atol=1e-12)
+
+
+def test_layer_forward_single_visible_key_routes_that_keys_value_row():
+    """Each query sees exactly one context key j(r). Its softmax weight is then 1, so the
+    attention output of query head h is the value row of key j(r) under KV head h // group.
+    One-hot target features and context_proj = sqrt(H) [I | 0 | 0] make the context rows
+    ctx[j] = sqrt(H) e_j exactly (their RMS is 1), so v_j = sqrt(H) v_proj[:, j]. With zero
+    embedding rows, o_proj = I and down_proj = 0, the output row is RMSNorm of the concatenated
+    head outputs. A wrong key, a wrong query-head to KV-head map or a lost residual changes it."""
+    H, D, hq, hkv, F, T, nq, V = 8, 2, 4, 2, 16, 6, 4, 3
+    P = _layer_params(H, D, hq, hkv, F, V)
+    P["embed_tokens"][:] = 0.0
+    P["context_proj"] = np.sqrt(H) * np.concatenate([np.eye(H), np.zeros((H, 2 * H))], axis=1)
+    M = np.array([[1, -2, 3, 0, 2, -1, 4, 1], [0, 1, -1, 2, 3, 1, -2, 2],
+                  [2, 0, 1, -3, 1, 2, 1, -1], [-1, 3, 0, 1, -2, 1, 2, 3]], np.float64)
+    P["v_proj"] = M
+    P["o_proj"] = np.eye(H)
+    P["down_proj"][:] = 0.0
+    th = np.zeros((1, T, 3 * H))
+    for j in range(T):
+        th[0, j, j] = 1.0
+    keys = [4, 1, 5, 0]  # the one visible context key of each query row
+    vis = np.zeros((nq, T + nq), bool)
+    for r, j in enumerate(keys):
+        vis[r, j] = True
+    eps = 1e-12
+    out = _run_layer(P, th, [0, 1, 2, 0], T, nq, vis, D, eps)
+    group = hq // hkv
+    for r, j in enumerate(keys):
+        v = np.sqrt(H) * M[:, j]  # [hkv * D]
+        y = np.concatenate([v[(h // group) * D:(h // group + 1) * D] for h in range(hq)])
+        want = y / np.sqrt((y * y).mean() + eps)
+        np.testing.assert_allclose(out[r], want, rtol=1e-9, atol=1e-12)
+
+
+def test_layer_forward_swiglu_gates_with_the_first_half():
+    """gate_up_proj rows [gate; up]: with the attention removed, constant positive embedding rows
+    normalise to ones, so gate = -50 and up = 1 for every unit. silu(-50) * 1 is ~1e-20, so the MLP
+    adds nothing and the output is final_norm(ones) = ones; gate and up swapped would add
+    silu(1) * -50 * sum(down) per dimension. With gate = 1 and up = 2 instead, the MLP adds
+    2 silu(1) (= 2 / (1 + e^-1)) times each down_proj row sum."""
+    H, D, hq, hkv, F, T, nq, V = 8, 4, 2, 1, 4, 3, 2, 2
+    P = _layer_params(H, D, hq, hkv, F, V)
+    P["embed_tokens"][:] = 2.0
+    P["o_proj"][:] = 0.0
+    down = _rng(8).standard_normal((H, F))
+    P["down_proj"] = down
+    vis = np.ones((nq, T + nq), bool)
+    th = _rng(9).standard_normal((1, T, 3 * H))
+    P["gate_up_proj"] = np.concatenate([np.full((F, H), -50.0 / H), np.full((F, H), 1.0 / H)])
+    out = _run_layer(P, th, [0, 1], T, nq, vis, D, 1e-12)
+    np.testing.assert_allclose(out, np.ones((nq, H)), rtol=1e-12)
+    P["gate_up_proj"] = np.concatenate([np.full((F, H), 1.0 / H), np.full((F, H), 2.0 / H)])
+    out = _run_layer(P, th, [0, 1], T, nq, vis, D, 1e-12)
+    y = 2.0 + 2.0 / (1.0 + math.exp(-1.0)) * down.sum(axis=1)
+    want = y / np.sqrt((y * y).mean() + 1e-12)
+    np.testing.assert_allclose(out, np.broadcast_to(want, (nq, H)), rtol=1e-12)
