@@ -27,6 +27,9 @@ two ragged 32K bins) and 4 (32K document, GQA 40/8) under "attention_configs" (s
 --no-attention-configs), and the full one-layer DSpark training step of BASELINE config 5 (forward,
 loss, backward and the fused AdamW) is timed on its own and reported under "config5_layer_step"
 (skip with --no-layer-step).
+After the timed work, "parity" compares the HIP outputs with the oracle on the bench's own
+config-2 inputs (every element of the attention outputs; 512 sampled loss rows), with max-abs and
+relative-L2 errors and the reference's tolerances (skip with --no-parity).
 Metric: input context tokens per second (4096 per step / wall time), as the reference's draft-only
 benchmark defines it (tools/performance/torchspec_benchmark.py:688,764).
 
@@ -59,6 +62,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the timed CPU oracle leg")
+    p.add_argument("--no-parity", action="store_true",
+                   help="skip the parity block (HIP outputs vs the oracle on the bench's own inputs)")
     p.add_argument("--no-kernel-timing", action="store_true", help="no per-kernel HIP events")
     p.add_argument("--no-attention-configs", action="store_true",
                    help="skip the attention-only timings at configs 3 and 4")
@@ -554,6 +559,121 @@ def cpu_baseline(x, seed):
     }
 
 
+def _errors(pairs):
+    """max-abs and relative-L2 over a list of (got, ref) CPU tensor pairs taken as one tensor."""
+    max_abs, num, den = 0.0, 0.0, 0.0
+    for got, ref in pairs:
+        diff = got.double() - ref.double()
+        if diff.numel():
+            max_abs = max(max_abs, float(diff.abs().max()))
+        num += float((diff * diff).sum())
+        den += float((ref.double() * ref.double()).sum())
+    return max_abs, (num ** 0.5) / max(den ** 0.5, 1e-30)
+
+
+def _within(pairs, atol, rtol):
+    return all(bool(((g.double() - r.double()).abs() <= atol + rtol * r.double().abs()).all())
+               for g, r in pairs)
+
+
+def parity_block(x, seed):
+    """Errors of the HIP path against the oracle on the bench's own config-2 inputs (outside the
+    timed region): attention O / LSE / dQ / dK / dV of every KV group against the chunked fp32
+    oracle (oracle/attention.py), with a seeded dO and LSE gradient; and CE / L1 / dlogits of the
+    fused loss on 512 sampled rows of the bench's own logits (head GEMM of the attention output,
+    indexed teacher table) against the fp64 oracle (oracle/loss.py). Tolerances are the
+    reference's (tests/test_thd_attention.py:218-225, tests/test_tiled_l1.py:28-46)."""
+    import torch
+
+    from aspec_amd.direct_cp import DirectCPMetadata, direct_cp_attention_from_kv
+    from aspec_amd.loss import ce_l1_from_logits
+    from aspec_amd.targets import dspark_targets
+    from oracle import attention as A
+    from oracle import loss as L
+    from oracle import metadata as M
+
+    t0 = time.perf_counter()
+    w = x["w"]
+    device = x["q"].device
+    anchors, keep, pos, docs, adocs = x["meta_tensors"]
+    meta = DirectCPMetadata(anchors, keep, pos, w.block_size, 0, 1, None, context_doc_ids=docs,
+                            anchor_doc_ids=adocs, sequence_length=w.sequence_length)
+    q, k, v = (x[n].detach().clone().requires_grad_() for n in ("q", "k", "v"))
+    g = torch.Generator().manual_seed(seed + 1)
+    dout = torch.randn(w.num_queries, w.q_heads, w.head_dim, generator=g).bfloat16()
+    dlse = torch.randn(w.q_heads, w.num_queries, generator=g) * 0.1
+    out, lse = direct_cp_attention_from_kv(q, k, v, meta)
+    ((out.float() * dout.to(device)[None].transpose(1, 2).float()).sum()
+     + (lse * dlse.to(device)[None]).sum()).backward()
+    torch.cuda.synchronize()
+    got = {"O": out.detach()[0].float().cpu(), "LSE": lse.detach()[0].cpu(), "dQ": q.grad[0].float().cpu(),
+           "dK": k.grad[0].float().cpu(), "dV": v.grad[0].float().cpu()}
+    qc, kc, vc = (t.detach()[0].float().cpu() for t in (x["q"], x["k"], x["v"]))
+    dt = dout.float().transpose(0, 1)
+    ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
+                       w.block_size, w.sequence_length)
+    group = w.q_heads // w.kv_heads
+    pairs = {n: [] for n in got}
+    for kv in range(w.kv_heads):
+        sl = slice(kv * group, (kv + 1) * group)
+        ref = A.attention_group_sampled(qc[sl], kc[kv], vc[kv], ends, w.head_dim ** -0.5, dt[sl],
+                                        dlse[sl], dq_rows=np.arange(w.num_queries),
+                                        key_ranges=[(0, w.num_keys)], chunk=256)
+        row_keep = ref["lse"][0] > A.MASK_VALUE / 2
+        pairs["O"].append((got["O"][sl], ref["out"]))
+        pairs["LSE"].append((got["LSE"][sl][:, row_keep], ref["lse"][:, row_keep]))
+        pairs["dQ"].append((got["dQ"][sl], ref["dq"]))
+        pairs["dK"].append((got["dK"][kv], ref["dkv"][0][0]))
+        pairs["dV"].append((got["dV"][kv], ref["dkv"][0][1]))
+    block = {"oracle": "oracle/attention.py attention_group_sampled (fp32) and oracle/loss.py (fp64)",
+             "inputs": "the bench's own config-2 Q/K/V and head; seeded dO and dLSE"}
+    ok = True
+    for name, tol in (("O", 0.025), ("LSE", 0.025), ("dQ", 0.04), ("dK", 0.04), ("dV", 0.04)):
+        max_abs, rel = _errors(pairs[name])
+        passed = _within(pairs[name], tol, tol)
+        ok &= passed
+        block[f"attention_{name}"] = {"max_abs": round(max_abs, 6), "rel_l2": round(rel, 7),
+                                      "atol": tol, "rtol": tol, "pass": passed,
+                                      "scope": f"all {w.kv_heads} KV groups, every element"}
+    # loss on the bench's own logits: the head GEMM of this attention output
+    with torch.no_grad():
+        hidden = out.detach().transpose(1, 2).reshape(w.num_queries, w.q_heads * w.head_dim)
+        logits = torch.matmul(hidden, x["head"].t()).contiguous()
+        teacher = torch.matmul(x["target_hidden"], x["head"].t()).contiguous()
+    targets = dspark_targets(anchors, keep, x["input_ids"], x["loss_mask"], w.block_size,
+                             loss_decay_gamma=DECAY_GAMMA, ctx_doc_ids=docs)
+    tid, tix = targets.target_ids.reshape(-1), targets.teacher_index.reshape(-1)
+    wts = targets.weights.reshape(-1)
+    xin = logits.clone().requires_grad_()
+    ce, l1 = ce_l1_from_logits(xin, tid, teacher, teacher_indices=tix)
+    gce, gl1 = CE_ALPHA * wts / wts.sum(), L1_ALPHA * wts / wts.sum()
+    ((ce * gce).sum() + (l1 * gl1).sum()).backward()
+    torch.cuda.synchronize()
+    rows = np.random.default_rng(seed).choice(w.num_queries, 512, replace=False)
+    ri = torch.as_tensor(rows, device=device)
+    xd = logits[ri].double().cpu().numpy()
+    yd = teacher[tix[ri]].double().cpu().numpy()
+    td = tid[ri].cpu().numpy()
+    ref_ce, ref_l1 = L.cross_entropy(xd, td), L.l1(xd, yd)
+    ref_g = (L.cross_entropy_grad(xd, td, gce[ri].double().cpu().numpy())
+             + L.l1_grad(xd, yd, gl1[ri].double().cpu().numpy()))
+    loss_pairs = {
+        "CE": ([(ce.detach()[ri].cpu(), torch.as_tensor(ref_ce))], 2e-5, 2e-6),
+        "L1": ([(l1.detach()[ri].cpu(), torch.as_tensor(ref_l1))], 2e-6, 2e-6),
+        "dlogits": ([(xin.grad[ri].cpu(), torch.as_tensor(ref_g).to(torch.bfloat16))], 1e-6, 0.02),
+    }
+    for name, (pr, atol, rtol) in loss_pairs.items():
+        max_abs, rel = _errors(pr)
+        passed = _within(pr, atol, rtol)
+        ok &= passed
+        block[f"loss_{name}"] = {"max_abs": float(f"{max_abs:.3e}"), "rel_l2": float(f"{rel:.3e}"),
+                                 "atol": atol, "rtol": rtol, "pass": passed,
+                                 "scope": f"512 sampled of {w.num_queries} rows x V={VOCAB}"}
+    block["pass"] = ok
+    block["seconds"] = round(time.perf_counter() - t0, 1)
+    return block
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -689,6 +809,8 @@ def main():
         result["attention_configs"] = attention_configs(device, max(3, args.steps // 4))
     if not args.no_layer_step:
         result["config5_layer_step"] = layer_step(device, max(3, args.steps // 2), 2)
+    if not args.no_parity:
+        result["parity"] = parity_block(x, args.seed)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(x, args.seed)
     print(json.dumps(result), flush=True)

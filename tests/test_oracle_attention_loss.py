@@ -114,3 +114,46 @@ def test_loss_gradients_match_finite_differences(fn):
         p[idx] += eps
         m[idx] -= eps
         assert abs((f(p) - f(m)) / (2 * eps) - grad[idx]) < 1e-7
+
+
+def test_sampled_group_oracle_equals_dense_oracle():
+    """`attention_group_sampled` (the chunked single-KV-group form used at config 4) against the
+    dense `attention` on a small ragged layout with a dropped block and an LSE gradient: O and
+    LSE for every row, dQ for sampled rows and dK/dV for key ranges that straddle the context /
+    draft boundary, all in float64, for several chunk sizes (chunk edges inside blocks)."""
+    w, q, k, v = _small()
+    ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
+                       w.block_size, w.sequence_length)
+    vis = M.endpoints_to_dense(ends, w.num_keys)
+    g = torch.Generator().manual_seed(3)
+    dout = torch.randn(4, w.num_queries, 16, generator=g, dtype=torch.float64)
+    dlse = torch.randn(4, w.num_queries, generator=g, dtype=torch.float64)
+    out, lse, (dq, dk, dv) = A.attention(q, k, v, vis, 0.3, dout=dout, dlse=dlse)
+    rows = [0, 3, 5, w.num_queries - 1]
+    ranges = [(0, 5), (w.context_length - 3, w.context_length + 4), (w.num_keys - 2, w.num_keys)]
+    for kv in range(2):
+        sl = slice(2 * kv, 2 * kv + 2)
+        for chunk in (3, 7, 64):
+            got = A.attention_group_sampled(q[sl], k[kv], v[kv], ends, 0.3, dout[sl], dlse[sl],
+                                            dq_rows=rows, key_ranges=ranges, chunk=chunk,
+                                            dtype=torch.float64)
+            torch.testing.assert_close(got["out"], out[sl], rtol=1e-12, atol=1e-12)
+            torch.testing.assert_close(got["lse"], lse[sl], rtol=1e-12, atol=1e-12)
+            torch.testing.assert_close(got["dq"], dq[sl][:, rows], rtol=1e-10, atol=1e-12)
+            for (k0, k1), (gk, gv) in zip(ranges, got["dkv"]):
+                torch.testing.assert_close(gk, dk[kv, k0:k1], rtol=1e-10, atol=1e-12)
+                torch.testing.assert_close(gv, dv[kv, k0:k1], rtol=1e-10, atol=1e-12)
+
+
+def test_dense_oracle_kv_head_subset_equals_full_run():
+    w, q, k, v = _small()
+    vis = _dense(w)
+    g = torch.Generator().manual_seed(4)
+    dout = torch.randn(4, w.num_queries, 16, generator=g, dtype=torch.float64)
+    full = A.attention(q, k, v, vis, 0.25, dout=dout)
+    part = A.attention(q, k, v, vis, 0.25, dout=dout, kv_heads=[1])
+    torch.testing.assert_close(part[0][2:], full[0][2:])
+    torch.testing.assert_close(part[1][2:], full[1][2:])
+    for a, b in zip(part[2], full[2]):
+        torch.testing.assert_close(a[2:] if a.shape[0] == 4 else a[1:], b[2:] if b.shape[0] == 4 else b[1:])
+    assert not part[0][:2].any()
