@@ -1,7 +1,7 @@
 """aspec_amd: MI355X-native (gfx950 HIP) DSpark draft hot path.
 
 Drop-in replacements for the reference operators of aspec/models/ops (direct CP / THD attention,
-THD sparse metadata, tiled L1, the selective-head losses, the fused Q/K RMSNorm + RoPE, the DSpark
+the cuDNN FlexAttention surface with its DSpark interval masks, THD sparse metadata, tiled L1, the selective-head losses, the fused Q/K RMSNorm + RoPE, the DSpark
 head terms with the Markov bias and confidence head), the work-aware row packing policy
 (aspec/controller/packing.py), the packing collator (aspec/data/utils.py), the anchor layout (anchors.py), output-block compaction (output_blocks.py)
 and the DSpark targets (dspark.py), backed by hand-written HIP kernels in libaspec_amd.so,
@@ -15,6 +15,12 @@ from aspec_amd.anchors import (  # noqa: F401
     validate_injected_anchors,
 )
 from aspec_amd.collate import DFlashPackingCollator  # noqa: F401
+from aspec_amd.cudnn_flex_attention import (  # noqa: F401
+    CudnnFlexMask,
+    build_dspark_mla_mask,
+    cudnn_flex_attention,
+    resolve_cudnn_gqa_mode,
+)
 from aspec_amd.direct_cp import (  # noqa: F401
     MASK_VALUE,
     DirectCPMetadata,
@@ -56,6 +62,10 @@ from aspec_amd.tiled_l1 import tiled_l1_from_logits  # noqa: F401
 
 __all__ = [
     "AcceptRatePredictor",
+    "CudnnFlexMask",
+    "build_dspark_mla_mask",
+    "cudnn_flex_attention",
+    "resolve_cudnn_gqa_mode",
     "DFlashPackingCollator",
     "PackingResult",
     "count_eligible_anchor_starts",

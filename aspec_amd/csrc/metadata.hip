@@ -48,10 +48,24 @@ struct RowArgs {
 };
 
 // One thread per query row q (which also owns draft key T+q, the same block and offset at CP=1),
-// followed by one thread per context key.
+// followed by one thread per context key; blockIdx.y is the batch row b. Inputs are [batch][...]
+// contiguous; outputs are the rows of all batch rows back to back: query_aux [4][B*Nq], key_aux
+// [4][B*K], endpoints [5][B*Nq] in the flattened key space (row b's keys are b*K .. b*K + K - 1;
+// dropped rows stay all zero), so one attention launch covers every batch row.
 __global__ void row_metadata_kernel(RowArgs a) {
   const int64_t nq = a.num_blocks * a.block;
   const int64_t K = a.T + nq;
+  const int64_t b = blockIdx.y;
+  const int64_t nb = gridDim.y;
+  a.anchors += b * a.num_blocks;
+  a.keep += b * a.num_blocks;
+  a.anchor_docs += b * a.num_blocks;
+  a.ctx_pos += b * a.T;
+  a.ctx_docs += b * a.T;
+  const int64_t qrow0 = b * nq;   // this batch row's first flattened query row
+  const int64_t key0 = b * K;     // and first flattened key
+  const int64_t NQ = nb * nq;     // flattened field strides
+  const int64_t NK = nb * K;
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (tid < nq) {
     const int64_t q = tid;
@@ -64,17 +78,17 @@ __global__ void row_metadata_kernel(RowArgs a) {
     const bool token_keep = block_keep && (a.seq_len <= 0 || anchor + o < a.seq_len);
     const bool query_keep = token_keep && doc >= 0;
     if (a.qaux) {
-      a.qaux[0 * nq + q] = static_cast<int32_t>(anchor);
-      a.qaux[1 * nq + q] = query_keep ? 1 : 0;
-      a.qaux[2 * nq + q] = static_cast<int32_t>(r);
-      a.qaux[3 * nq + q] = static_cast<int32_t>(doc);
+      a.qaux[0 * NQ + qrow0 + q] = static_cast<int32_t>(anchor);
+      a.qaux[1 * NQ + qrow0 + q] = query_keep ? 1 : 0;
+      a.qaux[2 * NQ + qrow0 + q] = static_cast<int32_t>(r);
+      a.qaux[3 * NQ + qrow0 + q] = static_cast<int32_t>(doc);
     }
     if (a.kaux) {  // _key_metadata draft half (thd_attention.py:42-56)
-      const int64_t kq = a.T + q;
-      a.kaux[0 * K + kq] = static_cast<int32_t>(doc);
-      a.kaux[1 * K + kq] = static_cast<int32_t>(-o - 1);
-      a.kaux[2 * K + kq] = static_cast<int32_t>(r);
-      a.kaux[3 * K + kq] = query_keep ? 1 : 0;
+      const int64_t kq = key0 + a.T + q;
+      a.kaux[0 * NK + kq] = static_cast<int32_t>(doc);
+      a.kaux[1 * NK + kq] = static_cast<int32_t>(-o - 1);
+      a.kaux[2 * NK + kq] = static_cast<int32_t>(r);
+      a.kaux[3 * NK + kq] = query_keep ? 1 : 0;
     }
     if (a.ends) {  // _build_cudnn_thd_mask (direct_cp.py:790-878)
       int64_t cb = 0, ce = 0, db = 0, de = 0;
@@ -99,21 +113,25 @@ __global__ void row_metadata_kernel(RowArgs a) {
           de = min(de, base + min(o + a.q_window, a.block));
         }
         db = min(db, de);
+        cb += key0;
+        ce += key0;
+        db += key0;
+        de += key0;
       }
-      a.ends[0 * nq + q] = 0;
-      a.ends[1 * nq + q] = static_cast<int32_t>(cb);
-      a.ends[2 * nq + q] = static_cast<int32_t>(ce);
-      a.ends[3 * nq + q] = static_cast<int32_t>(db);
-      a.ends[4 * nq + q] = static_cast<int32_t>(de);
+      a.ends[0 * NQ + qrow0 + q] = 0;
+      a.ends[1 * NQ + qrow0 + q] = static_cast<int32_t>(cb);
+      a.ends[2 * NQ + qrow0 + q] = static_cast<int32_t>(ce);
+      a.ends[3 * NQ + qrow0 + q] = static_cast<int32_t>(db);
+      a.ends[4 * NQ + qrow0 + q] = static_cast<int32_t>(de);
     }
   } else if (tid < nq + a.T) {
     const int64_t t = tid - nq;
     const int64_t doc = a.ctx_docs[t];
     if (a.kaux) {  // _key_metadata context half
-      a.kaux[0 * K + t] = static_cast<int32_t>(doc);
-      a.kaux[1 * K + t] = static_cast<int32_t>(a.ctx_pos[t]);
-      a.kaux[2 * K + t] = -1;
-      a.kaux[3 * K + t] = doc >= 0 ? 1 : 0;
+      a.kaux[0 * NK + key0 + t] = static_cast<int32_t>(doc);
+      a.kaux[1 * NK + key0 + t] = static_cast<int32_t>(a.ctx_pos[t]);
+      a.kaux[2 * NK + key0 + t] = -1;
+      a.kaux[3 * NK + key0 + t] = doc >= 0 ? 1 : 0;
     }
     if (a.flags && t > 0) {
       int bad = 0;
@@ -357,21 +375,26 @@ int launch_tile_metadata(const int32_t* ends, int64_t nq, int64_t nk, int64_t tm
 
 using namespace aspec;
 
-extern "C" int aspec_thd_row_metadata(const int64_t* anchors, const uint8_t* keep,
-                                      const int64_t* anchor_docs, const int64_t* context_positions,
-                                      const int64_t* context_docs, int64_t num_blocks,
-                                      int64_t block_size, int64_t context_length,
-                                      int64_t sequence_length, int64_t context_window,
-                                      int64_t query_window, int draft_is_causal,
-                                      int32_t* query_aux, int32_t* key_aux, int32_t* endpoints,
-                                      int32_t* status_flags, void* stream) {
-  if (num_blocks < 0 || block_size <= 0 || context_length < 0)
-    return set_error(ASPEC_ERR_INVALID, "invalid THD geometry (blocks=%lld, block=%lld, T=%lld)",
-                     (long long)num_blocks, (long long)block_size, (long long)context_length);
+extern "C" int aspec_thd_batch_row_metadata(const int64_t* anchors, const uint8_t* keep,
+                                            const int64_t* anchor_docs,
+                                            const int64_t* context_positions,
+                                            const int64_t* context_docs, int64_t batch,
+                                            int64_t num_blocks, int64_t block_size,
+                                            int64_t context_length, int64_t sequence_length,
+                                            int64_t context_window, int64_t query_window,
+                                            int draft_is_causal, int32_t* query_aux,
+                                            int32_t* key_aux, int32_t* endpoints,
+                                            int32_t* status_flags, void* stream) {
+  if (batch <= 0 || batch > 65535 || num_blocks < 0 || block_size <= 0 || context_length < 0)
+    return set_error(ASPEC_ERR_INVALID,
+                     "invalid THD geometry (batch=%lld, blocks=%lld, block=%lld, T=%lld)",
+                     (long long)batch, (long long)num_blocks, (long long)block_size,
+                     (long long)context_length);
   const int64_t nq = num_blocks * block_size;
   const int64_t K = context_length + nq;
-  if (K >= (1LL << 31) - 1)
-    return set_error(ASPEC_ERR_INVALID, "THD metadata exceeds int32 indexing (%lld keys)", (long long)K);
+  if (batch * K >= (1LL << 31) - 1)
+    return set_error(ASPEC_ERR_INVALID, "THD metadata exceeds int32 indexing (%lld keys)",
+                     (long long)(batch * K));
   if (num_blocks > 0 && (!anchors || !keep || !anchor_docs))
     return set_error(ASPEC_ERR_INVALID, "anchors, keep and anchor_docs are required");
   if (context_length > 0 && (!context_positions || !context_docs))
@@ -397,9 +420,24 @@ extern "C" int aspec_thd_row_metadata(const int64_t* anchors, const uint8_t* kee
   a.flags = status_flags;
   const int threads = 256;
   const int64_t blocks = (total + threads - 1) / threads;
-  hipLaunchKernelGGL(row_metadata_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(threads), 0,
-                     static_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(row_metadata_kernel,
+                     dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(batch)),
+                     dim3(threads), 0, static_cast<hipStream_t>(stream), a);
   return check_launch("row_metadata_kernel");
+}
+
+extern "C" int aspec_thd_row_metadata(const int64_t* anchors, const uint8_t* keep,
+                                      const int64_t* anchor_docs, const int64_t* context_positions,
+                                      const int64_t* context_docs, int64_t num_blocks,
+                                      int64_t block_size, int64_t context_length,
+                                      int64_t sequence_length, int64_t context_window,
+                                      int64_t query_window, int draft_is_causal,
+                                      int32_t* query_aux, int32_t* key_aux, int32_t* endpoints,
+                                      int32_t* status_flags, void* stream) {
+  return aspec_thd_batch_row_metadata(anchors, keep, anchor_docs, context_positions, context_docs,
+                                      1, num_blocks, block_size, context_length, sequence_length,
+                                      context_window, query_window, draft_is_causal, query_aux,
+                                      key_aux, endpoints, status_flags, stream);
 }
 
 extern "C" int aspec_thd_aux_endpoints(const int32_t* query_aux, const int32_t* key_aux,

@@ -158,16 +158,18 @@ def direct_cp_attention_observation(metadata: DirectCPMetadata) -> dict:
 # Integer metadata (HIP): THD mask tensors, interval endpoints and the attention plan.
 # ---------------------------------------------------------------------------------------------
 class ThdRows:
-    """Device-resident row metadata of one forward: query_aux [4,Nq], key_aux [4,K] (int32),
-    endpoints [5,Nq] (int32) and the layout status flags."""
+    """Device-resident row metadata of one forward: query_aux [4, B*Nq], key_aux [4, B*K] (int32),
+    endpoints [5, B*Nq] (int32, flattened key space: batch row b owns keys b*K .. b*K + K - 1) and
+    the layout status flags. num_queries / num_keys count all batch rows."""
 
-    def __init__(self, query_aux, key_aux, endpoints, flags, num_queries, num_keys):
+    def __init__(self, query_aux, key_aux, endpoints, flags, num_queries, num_keys, batch=1):
         self.query_aux = query_aux
         self.key_aux = key_aux
         self.endpoints = endpoints
         self.flags = flags
         self.num_queries = num_queries
         self.num_keys = num_keys
+        self.batch = batch
         self._checked = False
 
     def check_layout(self) -> None:
@@ -184,43 +186,47 @@ class ThdRows:
 
 
 def thd_row_metadata(metadata: DirectCPMetadata, device) -> ThdRows:
-    """HIP `aspec_thd_row_metadata`: `_query_metadata` / `_key_metadata`
-    (thd_attention.py:25-56) and `_build_cudnn_thd_mask` (direct_cp.py:750-900), cached per forward."""
+    """HIP `aspec_thd_batch_row_metadata`: `_query_metadata` / `_key_metadata`
+    (thd_attention.py:25-56) and `_build_cudnn_thd_mask` (direct_cp.py:750-900) for every batch
+    row at once, cached per forward. Batch > 1 is served for unpacked rows on every backend and
+    for packed rows on the cuDNN / HIP backends; packed rows on the FA4 path keep the reference's
+    one-row rule (thd_attention.py:141-142)."""
     device = torch.device(device)
     key = ("hip_thd_rows", device)
     rows = metadata._fa4_cache.thd_inputs.get(key)
     if rows is not None:
         return rows
-    if metadata.anchor_positions.shape[0] != 1:
+    batch = metadata.anchor_positions.shape[0]
+    if batch != 1 and metadata.context_doc_ids is not None and metadata.backend in {"fa4", "auto"}:
         raise ValueError("THD packing requires one controller-owned row per microbatch")
     if metadata.cp_size != 1:
         raise NotImplementedError("context parallelism > 1 needs several GPUs; this build is CP=1")
     n, block, T = metadata.num_blocks, metadata.block_size, metadata.context_length
     nq, nk = n * block, T + n * block
-    anchors = metadata.anchor_positions[0].to(device=device, dtype=torch.int64).contiguous()
-    keep = metadata.block_keep_mask[0].to(device=device, dtype=torch.bool).contiguous()
-    positions = metadata.context_position_ids[0].to(device=device, dtype=torch.int64).contiguous()
+    anchors = metadata.anchor_positions.to(device=device, dtype=torch.int64).contiguous()
+    keep = metadata.block_keep_mask.to(device=device, dtype=torch.bool).contiguous()
+    positions = metadata.context_position_ids.to(device=device, dtype=torch.int64).contiguous()
     if metadata.context_doc_ids is None:
-        # Unpacked row: one document (the reference's packed=False mask at direct_cp.py:540-545).
-        anchor_docs = torch.zeros(n, dtype=torch.int64, device=device)
-        context_docs = torch.zeros(T, dtype=torch.int64, device=device)
+        # Unpacked rows: one document each (the reference's packed=False mask, direct_cp.py:540-545).
+        anchor_docs = torch.zeros((batch, n), dtype=torch.int64, device=device)
+        context_docs = torch.zeros((batch, T), dtype=torch.int64, device=device)
     else:
-        anchor_docs = metadata.anchor_doc_ids[0].to(device=device, dtype=torch.int64).contiguous()
-        context_docs = metadata.context_doc_ids[0].to(device=device, dtype=torch.int64).contiguous()
-    query_aux = torch.empty((4, nq), dtype=torch.int32, device=device)
-    key_aux = torch.empty((4, nk), dtype=torch.int32, device=device)
-    endpoints = torch.empty((5, nq), dtype=torch.int32, device=device)
+        anchor_docs = metadata.anchor_doc_ids.to(device=device, dtype=torch.int64).contiguous()
+        context_docs = metadata.context_doc_ids.to(device=device, dtype=torch.int64).contiguous()
+    query_aux = torch.empty((4, batch * nq), dtype=torch.int32, device=device)
+    key_aux = torch.empty((4, batch * nk), dtype=torch.int32, device=device)
+    endpoints = torch.empty((5, batch * nq), dtype=torch.int32, device=device)
     flags = torch.zeros(1, dtype=torch.int32, device=device)
     seq = metadata.sequence_length if metadata.sequence_length is not None else 0
     with _timing.region("thd_row_metadata"):
         _lib.call(
-            "aspec_thd_row_metadata", _lib.ptr(anchors), _lib.ptr(keep), _lib.ptr(anchor_docs),
-            _lib.ptr(positions), _lib.ptr(context_docs), n, block, T, seq,
+            "aspec_thd_batch_row_metadata", _lib.ptr(anchors), _lib.ptr(keep), _lib.ptr(anchor_docs),
+            _lib.ptr(positions), _lib.ptr(context_docs), batch, n, block, T, seq,
             metadata.context_window or 0, metadata.query_window or 0, int(metadata.draft_is_causal),
             _lib.ptr(query_aux), _lib.ptr(key_aux), _lib.ptr(endpoints), _lib.ptr(flags),
             _lib.stream_handle(device),
         )
-    rows = ThdRows(query_aux, key_aux, endpoints, flags, nq, nk)
+    rows = ThdRows(query_aux, key_aux, endpoints, flags, batch * nq, batch * nk, batch)
     metadata._fa4_cache.thd_inputs[key] = rows
     return rows
 
@@ -351,15 +357,23 @@ def _backward_side_stream(device) -> torch.cuda.Stream:
     return stream
 
 
+def _join_batch(x: Tensor) -> Tensor:
+    """[B, H, L, D] -> [1, H, B*L, D] with batch row b's tokens at b*L .. b*L + L - 1 (a view when
+    the storage is token-major [B, L, H, D], a copy otherwise)."""
+    b, h, n, d = x.shape
+    return x.transpose(1, 2).reshape(1, b * n, h, d).transpose(1, 2)
+
+
 def dspark_attention(query: Tensor, key: Tensor, value: Tensor, metadata: DirectCPMetadata,
                      scale: float) -> tuple[Tensor, Tensor]:
-    """HIP block-sparse DSpark attention over one packed THD row: (out [1,Hq,Nq,D], lse [1,Hq,Nq])."""
+    """HIP block-sparse DSpark attention over the metadata's rows: (out [B,Hq,Nq,D], lse [B,Hq,Nq])."""
     if not query.is_cuda:
         raise ValueError("aspec_amd attention runs on the GPU; got a CPU tensor")
     if query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
         raise NotImplementedError("aspec_amd DSpark attention computes in bf16 (fp32 accumulation)")
-    if query.shape[0] != 1:
-        raise ValueError("THD packing requires one controller-owned row per microbatch")
+    batch = query.shape[0]
+    if batch != metadata.anchor_positions.shape[0]:
+        raise ValueError("query batch must match the metadata batch")
     if query.shape[1] % key.shape[1]:
         raise ValueError("THD query heads must be divisible by KV heads")
     if query.shape[2] != metadata.num_blocks * metadata.block_size:
@@ -367,7 +381,16 @@ def dspark_attention(query: Tensor, key: Tensor, value: Tensor, metadata: Direct
     rows = thd_row_metadata(metadata, query.device)
     rows.check_layout()
     plan = attention_plan(metadata, rows, query.device)
-    output, lse = _DSparkAttention.apply(query, key, value, rows.endpoints, plan, scale)
+    if batch == 1:
+        output, lse = _DSparkAttention.apply(query, key, value, rows.endpoints, plan, scale)
+    else:
+        # Every batch row in one launch: rows are concatenated into one token axis (a view of
+        # token-major [B, L, H, D] storage), and the endpoints already address the flattened keys.
+        output, lse = _DSparkAttention.apply(_join_batch(query), _join_batch(key), _join_batch(value),
+                                             rows.endpoints, plan, scale)
+        nq, hq = query.shape[2], query.shape[1]
+        output = output.transpose(1, 2).reshape(batch, nq, hq, output.shape[-1]).transpose(1, 2)
+        lse = lse[0].view(hq, batch, nq).permute(1, 0, 2)
     observation = direct_cp_attention_observation(metadata)
     observation.update(
         qkv_format="thd", kernel_backend="hip", kernel_mode="block_sparse_interval",

@@ -62,6 +62,24 @@ int aspec_thd_row_metadata(const int64_t* anchors, const uint8_t* keep, const in
                            int32_t* endpoints, int32_t* status_flags, void* stream);
 
 /*
+ * aspec_thd_row_metadata for `batch` rows at once (unpacked or packed batch > 1, the rows
+ * `DirectCPMetadata` carries as [batch, ...] tensors, aspec/models/ops/direct_cp.py:147-262, and
+ * `_build_cudnn_thd_mask` builds for one cuDNN THD call, direct_cp.py:750-900). Inputs are
+ * [batch][N] / [batch][T] contiguous. Outputs hold every batch row back to back: query_aux
+ * [4][batch*Nq], key_aux [4][batch*K], endpoints [5][batch*Nq] in the flattened key space (row b's
+ * keys are b*K .. b*K + K - 1, its queries b*Nq .. b*Nq + Nq - 1; dropped rows stay all zero), so one
+ * attention launch serves the whole batch. batch = 1 is aspec_thd_row_metadata.
+ */
+int aspec_thd_batch_row_metadata(const int64_t* anchors, const uint8_t* keep,
+                                 const int64_t* anchor_docs, const int64_t* context_positions,
+                                 const int64_t* context_docs, int64_t batch, int64_t num_blocks,
+                                 int64_t block_size, int64_t context_length,
+                                 int64_t sequence_length, int64_t context_window,
+                                 int64_t query_window, int draft_is_causal, int32_t* query_aux,
+                                 int32_t* key_aux, int32_t* endpoints, int32_t* status_flags,
+                                 void* stream);
+
+/*
  * Interval endpoints [5][Nq] recovered from the eight THD mask tensors (query_aux [4][Nq],
  * key_aux [4][K], the layout of `_query_metadata` / `_key_metadata` at CP=1, context keys first).
  * This is the input `_classify_tiles` consumes (aspec/models/ops/thd_sparse_metadata.py:20-94);
@@ -91,6 +109,41 @@ int aspec_thd_tile_metadata(const int32_t* endpoints, int64_t num_queries, int64
                             int32_t* fwd_full_cnt, int32_t* fwd_full_idx,
                             int32_t* bwd_partial_cnt, int32_t* bwd_partial_idx,
                             int32_t* bwd_full_cnt, int32_t* bwd_full_idx, void* stream);
+
+/*
+ * The DSpark interval-union mask of the cuDNN FlexAttention path: `build_dspark_mla_mask`
+ * (aspec/models/ops/cudnn_flex_attention.py:53-170) with `_document_run_starts` (33-50).
+ * anchors int64 / keep uint8 [batch][num_anchors]; ctx_doc_ids int64 [batch][context_length] or
+ * NULL; sliding_window / context_window <= 0 mean None. Writes mask_func int32 [E][batch*Nq]
+ * (Nq = num_anchors * block_size) in each batch row's own key space: E = 3, (context_end,
+ * draft_begin, draft_end), without documents and windows, else E = 5, (0, context_begin,
+ * context_end, draft_begin, draft_end); rows of dropped blocks are all zero. *status_flags
+ * (caller-zeroed) gets bit 1 for an anchor outside [0, context_length) and bit 2 for a document
+ * id with more than one run in a batch row (the reference's two ValueErrors). workspace:
+ * aspec_dspark_mla_mask_workspace_bytes (needed with ctx_doc_ids).
+ */
+int aspec_dspark_mla_mask_workspace_bytes(int64_t batch, int64_t context_length, size_t* bytes);
+int aspec_dspark_mla_mask(const int64_t* anchors, const uint8_t* keep, const int64_t* ctx_doc_ids,
+                          int64_t batch, int64_t num_anchors, int64_t block_size,
+                          int64_t context_length, int is_causal, int64_t sliding_window,
+                          int64_t context_window, int32_t* mask_func, void* workspace,
+                          int32_t* status_flags, void* stream);
+
+/*
+ * An interval-union mask in the cuDNN FlexAttention format (`CudnnFlexMask.mask_func`,
+ * aspec/models/ops/cudnn_flex_attention.py:173-215, consumed by `cudnn_flex_attention` 331-440)
+ * turned into the attention kernels' endpoints. mask_func int32 [E][rows], E odd <= 9: row r sees
+ * keys [0, e0) and [e(2i-1), e(2i)) of its own sequence. BSHD (cu_seqlens NULL): rows are
+ * batch x query_length and sequence b owns keys b*key_length ..; THD: cu_seqlens_q / cu_seqlens_k
+ * int32 [num_segments + 1] give each segment's rows and keys. Writes endpoints int32 [5][rows]
+ * (0, cb, ce, db, de) in the flattened key space. *status_flags (caller-zeroed): bit 1 an endpoint
+ * outside [0, sequence keys]; bit 2 a row whose visible keys form more than two disjoint
+ * intervals (beyond the kernels' two-interval form); bit 4 a row outside every THD segment.
+ */
+int aspec_flex_mask_intervals(const int32_t* mask_func, int64_t num_endpoints, int64_t rows,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                              int64_t num_segments, int64_t query_length, int64_t key_length,
+                              int32_t* endpoints, int32_t* status_flags, void* stream);
 
 /*
  * Attention plan: the tile lists the attention kernels traverse, built once per forward and shared
