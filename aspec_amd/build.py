@@ -31,6 +31,9 @@ COMMON_FLAGS = [
     "-munsafe-fp-atomics",
     # Packed FP32 (v_pk_*_f32) stays off: scalar fp32 code only.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Run LLVM's machine verifier on the device code: an instruction selected with an operand of
+    # the wrong register class fails the build instead of being encoded silently.
+    "-mllvm", "-verify-machineinstrs",
 ]
 # The loss kernels must evaluate draft and teacher probabilities with identical instruction
 # sequences; contraction into FMAs stays off there.

@@ -255,9 +255,11 @@ __device__ __forceinline__ void store_row_c(uint16_t* dst, const f32x16 (&acc)[4
 // defeats loading two iterations ahead. Callers wait for them explicitly (vmcnt). The compiler's
 // own vector loads are issued before or after these and return in order, so its waits stay
 // correct (at worst they also cover these loads). M0 is written one instruction before its use.
+// The LDS byte address of a pointer into __shared__ memory: the low 32 bits of its flat address
+// (the shared aperture occupies the high half). Taken without an address-space cast, whose null
+// check the compiler can otherwise lower into an illegal compare against src_shared_base.
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
-  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-      (const __attribute__((address_space(3))) char*)(p))));
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
 }
 __device__ __forceinline__ void lds_load16(const void* src, void* lds_wave_base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
@@ -423,7 +425,7 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) {
   ListWindow lw{a.plan.f_list + m * a.plan.nnf, a.plan.f_cnt[m], 0, 0};
   lw.load(0, lane);
   const KvTileLanes lanes(lane);
-  auto issue = [&](uint32_t entry, KvStageFwd& stage) {
+  auto issue = [&](uint32_t entry, KvStageFwd& stage) __attribute__((always_inline)) {
     const int key0 = static_cast<int>(entry & ~kFullBit) * kTN;
     issue_kv_tile<G>(kbase, a.kst, vbase, a.vst, key0, nk, stage, wave, lanes);
   };
@@ -583,7 +585,7 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
   ListWindow lw{a.plan.f_list + m * a.plan.nnf, a.plan.f_cnt[m], 0, 0};
   lw.load(0, lane);
   const KvTileLanes lanes(lane);
-  auto issue = [&](uint32_t entry, int stage) {
+  auto issue = [&](uint32_t entry, int stage) __attribute__((always_inline)) {
     const int key0 = static_cast<int>(entry & ~kFullBit) * kTN;
     issue_kv_tile<G>(kbase, a.kst, vbase, a.vst, key0, nk, ring[stage], wave, lanes);
   };

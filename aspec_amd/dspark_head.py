@@ -189,13 +189,20 @@ def dspark_prediction_terms(hidden, target_ids, prev_ids, head_weight, aligned_t
                             eval_mask, weights, *, markov_head=None, confidence_head=None,
                             confidence_head_with_markov=True, l1_loss_alpha=1.0,
                             confidence_head_alpha=0.0, prediction_start=0, block_size=None,
-                            cached_target_logits=None, cached_draft_logits=None):
+                            cached_target_logits=None, cached_draft_logits=None,
+                            cached_target_positions=None, loss_cache=None):
     """Additive DSpark head terms for one block slice (aspec/models/dspark.py:553-636):
     (ce_num, l1_num, conf_num, position_loss, position_correct, acceptance_totals).
 
     hidden [B, N, K, H], target_ids / prev_ids [B, N, K], eval_mask / weights [B, N, K]. The
-    teacher logits are `cached_target_logits` (same shape as the logits) or aligned_target_hidden
-    projected by head_weight (no Markov bias), as in the reference's unsampled L1 path.
+    teacher logits are, as in the reference's unsampled L1 path:
+      - with `cached_target_positions` [B, N, K]: rows of the teacher table `cached_target_logits`
+        [B, context, V] at those context positions, read through int64 row indices by the loss
+        kernel itself (the indexed teacher of dspark.py:576-585; never gathered into a copy);
+      - else `cached_target_logits` (the logits' shape) or aligned_target_hidden projected by
+        head_weight (no Markov bias).
+    `loss_cache` is the head chunk's checkpoint-replay dict (dspark.py:473, 602): filled by the
+    first forward, replayed without a loss forward kernel on the checkpoint recompute.
     """
     if cached_draft_logits is not None:
         logits = cached_draft_logits
@@ -207,16 +214,26 @@ def dspark_prediction_terms(hidden, target_ids, prev_ids, head_weight, aligned_t
         logits = F.linear(hidden.reshape(-1, hidden.shape[-1]), head_weight).view(
             *hidden.shape[:-1], head_weight.shape[0])
     vocab = logits.shape[-1]
-    teacher = None
+    teacher = teacher_index = None
     if aligned_target_hidden is not None:
-        teacher = cached_target_logits if cached_target_logits is not None else F.linear(
-            aligned_target_hidden.reshape(-1, aligned_target_hidden.shape[-1]), head_weight
-        ).view_as(logits)
-        teacher = teacher.detach().contiguous()
+        if cached_target_positions is not None:
+            if cached_target_logits is None or cached_target_logits.ndim != 3:
+                raise ValueError("cached_target_positions index a [batch, context, vocab] teacher table")
+            batch, context, _ = cached_target_logits.shape
+            positions = cached_target_positions.flatten(1).long()
+            if batch > 1:
+                positions = positions + torch.arange(batch, device=positions.device)[:, None] * context
+            teacher_index = positions.reshape(-1).contiguous()
+            teacher = cached_target_logits.detach().reshape(-1, vocab).contiguous()
+        else:
+            teacher = cached_target_logits if cached_target_logits is not None else F.linear(
+                aligned_target_hidden.reshape(-1, aligned_target_hidden.shape[-1]), head_weight
+            ).view_as(logits)
+            teacher = teacher.detach().contiguous().reshape(-1, vocab)
     flat = logits.reshape(-1, vocab).contiguous()
     ce, l1, argmax = ce_l1_from_logits(
-        flat, target_ids.reshape(-1).long().contiguous(),
-        None if teacher is None else teacher.reshape(-1, vocab), return_argmax=True)
+        flat, target_ids.reshape(-1).long().contiguous(), teacher, teacher_indices=teacher_index,
+        return_argmax=True, _replay_cache=loss_cache)
     ce = ce.view_as(weights)
     ce_num = (ce * weights).sum()
     l1_num = logits.new_zeros((), dtype=torch.float32)

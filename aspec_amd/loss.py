@@ -56,38 +56,55 @@ def _check_logits(logits):
 
 class _CeL1(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, logits, targets, teacher, indices, ignore_index, want_argmax=False):
+    def forward(ctx, logits, targets, teacher, indices, ignore_index, want_argmax=False, replay_cache=None):
         vocab = logits.shape[-1]
         rows = logits.numel() // vocab
         dev = logits.device
-        stats = torch.empty((rows, STATS), dtype=torch.float32, device=dev)
-        ce = torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev)
-        l1 = torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev) if teacher is not None else None
-        flags = torch.zeros(1, dtype=torch.int32, device=dev)
         trows = teacher.shape[0] if (teacher is not None and indices is not None) else rows
-        amax = torch.empty(logits.shape[:-1], dtype=torch.int64, device=dev) if want_argmax else None
-        with _timing.region("loss_fwd"):
-            _lib.call("aspec_ce_l1_argmax_fwd", _lib.ptr(logits), _lib.ptr(teacher), _lib.ptr(indices),
-                      trows, _lib.ptr(targets), ignore_index, rows, vocab, _lib.ptr(l1), _lib.ptr(ce),
-                      _lib.ptr(amax), _lib.ptr(stats), _lib.ptr(flags), _lib.stream_handle(dev))
+        ctx.index_check = None
+        if replay_cache:
+            # Checkpoint replay of the same head chunk (the logits are recomputed bit for bit): the
+            # first forward's statistics and per-row results are reused and no forward kernel runs
+            # (the role of tiled_l1.py:134-139 for L1, here for CE, L1 and argmax together).
+            stats, ce, l1, amax = replay_cache["statistics"]
+            if (ce.shape != logits.shape[:-1] or stats.device != dev or replay_cache["vocab"] != vocab
+                    or (l1 is None) != (teacher is None) or (want_argmax and amax is None)):
+                raise ValueError("L1 checkpoint statistics belong to a different head chunk")
+        else:
+            stats = torch.empty((rows, STATS), dtype=torch.float32, device=dev)
+            ce = torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev)
+            l1 = torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev) if teacher is not None else None
+            flags = torch.zeros(1, dtype=torch.int32, device=dev)
+            amax = torch.empty(logits.shape[:-1], dtype=torch.int64, device=dev) if want_argmax else None
+            with _timing.region("loss_fwd"):
+                _lib.call("aspec_ce_l1_argmax_fwd", _lib.ptr(logits), _lib.ptr(teacher), _lib.ptr(indices),
+                          trows, _lib.ptr(targets), ignore_index, rows, vocab, _lib.ptr(l1), _lib.ptr(ce),
+                          _lib.ptr(amax), _lib.ptr(stats), _lib.ptr(flags), _lib.stream_handle(dev))
+            ctx.index_check = IndexCheck(flags)
+            if not ctx.needs_input_grad[0]:
+                ctx.index_check.raise_if_bad()
+            if replay_cache is not None:
+                replay_cache["statistics"] = (stats, ce.detach(), None if l1 is None else l1.detach(),
+                                              amax)
+                replay_cache["vocab"] = vocab
         ctx.save_for_backward(logits, targets, teacher, indices, stats)
         ctx.ignore_index = ignore_index
         ctx.trows = trows
-        ctx.index_check = IndexCheck(flags)
-        if not ctx.needs_input_grad[0]:
-            ctx.index_check.raise_if_bad()
         ctx.set_materialize_grads(False)
-        if l1 is None:
-            l1 = torch.zeros_like(ce)
-        if amax is None:
+        # new views keep the cached tensors free of this call's grad_fn
+        ce = ce.view_as(ce)
+        l1 = torch.zeros_like(ce) if l1 is None else l1.view_as(l1)
+        if not want_argmax:
             return ce, l1
+        amax = amax.view_as(amax)
         ctx.mark_non_differentiable(amax)
         return ce, l1, amax
 
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_ce, grad_l1, grad_argmax=None):
-        ctx.index_check.raise_if_bad()
+        if ctx.index_check is not None:
+            ctx.index_check.raise_if_bad()
         logits, targets, teacher, indices, stats = ctx.saved_tensors
         vocab = logits.shape[-1]
         rows = logits.numel() // vocab
@@ -95,20 +112,24 @@ class _CeL1(torch.autograd.Function):
         gl1 = None if (grad_l1 is None or teacher is None) else grad_l1.to(torch.float32).contiguous()
         grad_logits = torch.empty_like(logits)
         if gce is None and gl1 is None:
-            return grad_logits.zero_(), None, None, None, None, None
+            return grad_logits.zero_(), None, None, None, None, None, None
         with _timing.region("loss_bwd"):
             _lib.call("aspec_ce_l1_bwd", _lib.ptr(logits), _lib.ptr(teacher), _lib.ptr(indices),
                       ctx.trows, _lib.ptr(targets), ctx.ignore_index, rows, vocab, _lib.ptr(stats),
                       _lib.ptr(gl1), _lib.ptr(gce), _lib.ptr(grad_logits),
                       _lib.stream_handle(logits.device))
-        return grad_logits, None, None, None, None, None
+        return grad_logits, None, None, None, None, None, None
 
 
 def ce_l1_from_logits(logits, targets, teacher=None, *, teacher_indices=None, ignore_index=-100,
-                      return_argmax=False):
+                      return_argmax=False, _replay_cache=None):
     """Per-row (cross-entropy, softmax-L1) from bf16 logits in one pass (HIP). With
     `return_argmax`, also the row argmax (torch.argmax semantics: the first NaN, else the first
-    maximum) from the same pass, for the head's accuracy metric (dspark.py:625)."""
+    maximum) from the same pass, for the head's accuracy metric (dspark.py:625).
+
+    `_replay_cache` is the head chunk's checkpoint-replay dict (`loss_cache`, dspark.py:473,602):
+    an empty dict receives this forward's statistics and results; a filled one is replayed
+    without a forward kernel (the recomputed logits of a checkpoint replay are bitwise the same)."""
     _check_logits(logits)
     rows = logits.numel() // logits.shape[-1]
     if targets.dtype != torch.int64 or targets.numel() != rows or targets.device != logits.device:
@@ -129,7 +150,8 @@ def ce_l1_from_logits(logits, targets, teacher=None, *, teacher_indices=None, ig
                              "int64 index per Draft row")
         if teacher_indices is not None:
             teacher_indices = teacher_indices.reshape(-1).contiguous()
-    return _CeL1.apply(logits, targets, teacher, teacher_indices, ignore_index, return_argmax)
+    return _CeL1.apply(logits, targets, teacher, teacher_indices, ignore_index, return_argmax,
+                       _replay_cache)
 
 
 def cross_entropy(logits, targets, ignore_index=-100):

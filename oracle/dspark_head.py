@@ -69,9 +69,10 @@ def acceptance_statistics(accept, mask):
 
 def prediction_terms(h, target_ids, prev_ids, w, teacher_h, eval_mask, weights, *, w1=None, w2=None,
                      conf_w=None, conf_b=0.0, conf_with_markov=True, l1_alpha=1.0, conf_alpha=0.0,
-                     prediction_start=0):
+                     prediction_start=0, teacher_logits=None):
     """(ce_num, l1_num, conf_num, position_loss, position_correct, acceptance_totals) for
-    h [B, N, K, H] (dspark.py:553-636, unsampled L1 path, teacher = teacher_h W^T)."""
+    h [B, N, K, H] (dspark.py:553-636, unsampled L1 path, teacher = teacher_h W^T, or the
+    given teacher_logits rows [B*N*K, V] when teacher_h is None)."""
     h = np.asarray(h, np.float64)
     shape = h.shape[:-1]
     rows = h.reshape(-1, h.shape[-1])
@@ -87,8 +88,11 @@ def prediction_terms(h, target_ids, prev_ids, w, teacher_h, eval_mask, weights, 
     ce_num = (ce * weights).sum()
     l1_num = 0.0
     accept = None
-    if teacher_h is not None:
-        teacher = np.asarray(teacher_h, np.float64).reshape(-1, h.shape[-1]) @ np.asarray(w, np.float64).T
+    if teacher_h is not None or teacher_logits is not None:
+        if teacher_h is not None:
+            teacher = np.asarray(teacher_h, np.float64).reshape(-1, h.shape[-1]) @ np.asarray(w, np.float64).T
+        else:
+            teacher = np.asarray(teacher_logits, np.float64).reshape(logits.shape)
         l1 = oloss.l1(logits, teacher).reshape(shape)
         if l1_alpha > 0:
             l1_num = (l1 * weights).sum()

@@ -111,10 +111,12 @@ def test_config1_head_major_inputs_without_dlse(gpu):
     _check(W.config1(1), gpu, seed=1, token_major=False, use_dlse=False)
 
 
-def test_gqa_group_of_five(gpu):
+@pytest.mark.parametrize("group", [1, 2, 3, 5, 6, 7, 8])
+def test_every_gqa_group(gpu, group):
+    """Every compiled GQA group size (Hq / Hkv = 1..8; 4 is config 1-3's) on a config-1 layout."""
     w = W.config1(2)
-    w.q_heads, w.kv_heads = 10, 2
-    _check(w, gpu, seed=2)
+    w.q_heads, w.kv_heads = 2 * group, 2
+    _check(w, gpu, seed=2 + group)
 
 
 def test_no_active_queries_gives_zero_outputs_and_gradients(gpu):

@@ -155,3 +155,69 @@ def test_prediction_terms_match_oracle(gpu):
             assert np.abs(got - want).sum() <= 2
         else:
             np.testing.assert_allclose(got, want, rtol=2e-2, atol=2e-2)
+
+
+def test_prediction_terms_indexed_teacher_and_checkpoint_replay(gpu):
+    """The production path of _prediction_terms (aspec/models/dspark.py:573-605): teacher rows
+    read from the cached [batch, context, V] teacher table through cached_target_positions (batch 2,
+    so the per-row offsets b * context apply), against (a) the same terms with the rows gathered
+    into a copy (bitwise equal: the loss reads the same values) and (b) the fp64 oracle; then a
+    checkpoint replay through loss_cache reuses the first forward's statistics (no loss forward
+    kernel runs) and gives bitwise the same terms and gradient."""
+    from aspec_amd import _timing
+
+    B, N, K, H, V, C = 2, 5, 16, 128, 1024, 48
+    gen = torch.Generator(device=gpu).manual_seed(31)
+    rnd = lambda *s, scale=1.0: (torch.randn(*s, device=gpu, generator=gen) * scale).to(torch.bfloat16)  # noqa: E731
+    h = rnd(B, N, K, H, scale=0.5)
+    w = rnd(V, H, scale=0.05)
+    table = rnd(B, C, V, scale=2.0)
+    positions = torch.randint(0, C, (B, N, K), device=gpu, generator=gen)
+    tgt = torch.randint(0, V, (B, N, K), device=gpu, generator=gen)
+    prev = torch.randint(0, V, (B, N, K), device=gpu, generator=gen)
+    mask = (torch.rand(B, N, K, device=gpu, generator=gen) > 0.2).float()
+    weights = mask * torch.exp(-torch.arange(K, device=gpu) / 4.0)
+    gathered = table.gather(1, positions.flatten(1).unsqueeze(-1).expand(-1, -1, V)).view(B, N, K, V)
+    aligned = torch.zeros(B, N, K, H, device=gpu, dtype=torch.bfloat16)  # presence switches L1 on
+
+    def run(**teacher):
+        hh = h.clone().requires_grad_()
+        terms = dspark_prediction_terms(hh, tgt, prev, w, aligned, mask, weights, prediction_start=1,
+                                        **teacher)
+        (terms[0] * 0.1 + terms[1] * 0.9).backward()
+        return [t.detach().clone() for t in terms], hh.grad
+
+    indexed, g_indexed = run(cached_target_logits=table, cached_target_positions=positions)
+    copied, g_copied = run(cached_target_logits=gathered)
+    for a, b in zip(indexed, copied):
+        assert torch.equal(a, b)
+    assert torch.equal(g_indexed, g_copied)
+    np_ = lambda a: a.detach().double().cpu().numpy()  # noqa: E731
+    ref = odh.prediction_terms(np_(h), np_(tgt).astype(np.int64), np_(prev).astype(np.int64), np_(w), None,
+                               np_(mask), np_(weights), teacher_logits=np_(gathered).reshape(-1, V),
+                               prediction_start=1)
+    for name, got, want in zip(["ce_num", "l1_num", "conf_num", "position_loss", "position_correct",
+                                "acceptance"], indexed, ref):
+        got = np.asarray(np_(got), np.float64)
+        if name == "position_correct":
+            assert np.abs(got - want).sum() <= 2
+        else:
+            np.testing.assert_allclose(got, want, rtol=2e-2, atol=2e-2)
+    cache = {}
+    _timing.reset()
+    _timing.enable(True)
+    try:
+        first, g_first = run(cached_target_logits=table, cached_target_positions=positions, loss_cache=cache)
+        assert "statistics" in cache and _timing.summary()["loss_fwd"]["launches"] == 1
+        replay, g_replay = run(cached_target_logits=table, cached_target_positions=positions, loss_cache=cache)
+        assert _timing.summary()["loss_fwd"]["launches"] == 1  # the replay ran no forward kernel
+    finally:
+        _timing.enable(False)
+        _timing.reset()
+    for a, b, c in zip(first, replay, indexed):
+        assert torch.equal(a, b) and torch.equal(a, c)
+    assert torch.equal(g_first, g_replay) and torch.equal(g_first, g_indexed)
+    with pytest.raises(ValueError, match="different head chunk"):
+        dspark_prediction_terms(h[:, :2], tgt[:, :2], prev[:, :2], w, aligned[:, :2], mask[:, :2],
+                                weights[:, :2], cached_target_logits=table,
+                                cached_target_positions=positions[:, :2], loss_cache=cache)

@@ -75,7 +75,7 @@ def test_row_metadata_bit_exact(gpu, w, masks):
 
 
 @pytest.mark.parametrize("w", LAYOUTS, ids=lambda w: w.name)
-@pytest.mark.parametrize("masks", MASKS[:3], ids=str)
+@pytest.mark.parametrize("masks", MASKS, ids=str)
 @pytest.mark.parametrize("tile", [(256, 128), (256, 80), (256, 64), (32, 64), (32, 128), (5, 3)])
 def test_sparse_pair_from_aux_bit_exact(gpu, w, masks, tile, monkeypatch):
     """build_thd_sparse_pair on the eight mask tensors == brute-force any/all classes
@@ -123,3 +123,34 @@ def test_layout_violations_fail_closed(gpu):
     rows = thd_row_metadata(meta, gpu)
     with pytest.raises(ValueError, match="monotonically"):
         rows.check_layout()
+
+
+@pytest.mark.parametrize("masks", MASKS, ids=str)
+def test_batched_row_metadata_bit_exact(gpu, masks):
+    """aspec_thd_batch_row_metadata over three packed rows of one common geometry (the
+    DirectCPMetadata [batch, ...] form): each row's aux tensors and endpoints equal the oracle's for
+    that row, the endpoints shifted into the flattened key space (row b's keys start at b*K) and
+    dropped rows all zero."""
+    from aspec_amd.direct_cp import DirectCPMetadata
+
+    rows = [W.reference_test_layout(7), W.reference_test_layout(7, drop_doc=False),
+            W.reference_test_layout(7, lengths=(100, 400, 39))]
+    n, T = rows[0].num_blocks, rows[0].context_length
+    assert all(w.num_blocks == n and w.context_length == T for w in rows)
+    t = lambda key, dt: torch.as_tensor(np.stack([getattr(w, key) for w in rows]), dtype=dt, device=gpu)  # noqa: E731
+    meta = DirectCPMetadata(t("anchors", torch.long), t("keep", torch.bool), t("context_positions", torch.long),
+                            7, 0, 1, None, context_doc_ids=t("ctx_doc_ids", torch.long),
+                            anchor_doc_ids=t("anchor_doc_ids", torch.long), sequence_length=T,
+                            backend="cudnn_flex_attention", **masks)
+    got = thd_row_metadata(meta, gpu)
+    torch.cuda.synchronize()
+    nq, nk = rows[0].num_queries, rows[0].num_keys
+    assert got.num_queries == 3 * nq and got.num_keys == 3 * nk and int(got.flags.item()) == 0
+    for b, w in enumerate(rows):
+        qaux, kaux, ends = _oracle(w, **masks)
+        np.testing.assert_array_equal(got.query_aux[:, b * nq:(b + 1) * nq].cpu().numpy(), qaux)
+        np.testing.assert_array_equal(got.key_aux[:, b * nk:(b + 1) * nk].cpu().numpy(), kaux)
+        kept = ends[2] > ends[1]
+        kept |= ends[4] > ends[3]
+        shifted = np.where(kept[None], ends + np.array([0, 1, 1, 1, 1])[:, None] * b * nk, 0)
+        np.testing.assert_array_equal(got.endpoints[:, b * nq:(b + 1) * nq].cpu().numpy(), shifted)

@@ -151,3 +151,16 @@ def test_prediction_terms_conf_num_and_position_correct_hand_computed():
     # the acceptance totals see alpha = accept * mask: per position [2, 2, 0] and tau = 1 + 1 + 1
     # for both blocks (the cumulative product stops at position 2)
     np.testing.assert_allclose(out[5], [[2.0, 2.0, 0.0, 6.0], [2.0, 2.0, 1.0, 2.0]], atol=1e-12)
+
+
+def test_prediction_terms_teacher_logits_equal_projected_teacher():
+    r = _rng(9)
+    B, N, K, H, V = 1, 2, 3, 4, 6
+    h, th = r.standard_normal((B, N, K, H)), r.standard_normal((B, N, K, H))
+    w = r.standard_normal((V, H))
+    tgt, prev = r.integers(0, V, (B, N, K)), r.integers(0, V, (B, N, K))
+    mask = np.ones((B, N, K))
+    a = odh.prediction_terms(h, tgt, prev, w, th, mask, mask)
+    b = odh.prediction_terms(h, tgt, prev, w, None, mask, mask, teacher_logits=th.reshape(-1, H) @ w.T)
+    for x, y in zip(a, b):
+        np.testing.assert_allclose(x, y, rtol=1e-12)
