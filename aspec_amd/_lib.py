@@ -88,6 +88,10 @@ SIGNATURES = {
         _int, [_c_void_p] * 11 + [_i64, _i64] + [_c_void_p] * 3 + [_i64] * 6 + [_f32]
         + [_c_void_p] * 8
     ),
+    "aspec_qk_norm_rope_bwd_noalloc": (
+        _int, [_c_void_p] * 11 + [_i64, _i64] + [_c_void_p] * 3 + [_i64] * 6 + [_f32]
+        + [_c_void_p] * 7
+    ),
     "aspec_rmsnorm_fwd": (_int, [_c_void_p] * 3 + [_i64, _i64, _f32] + [_c_void_p] * 4),
     "aspec_rmsnorm_bwd_workspace_bytes": (_int, [_i64, _c_void_p]),
     "aspec_rmsnorm_bwd": (_int, [_c_void_p] * 5 + [_i64, _i64] + [_c_void_p] * 4),

@@ -12,6 +12,8 @@
 //
 // Lane layout: 16 lanes per head row; lane j holds dims 4j..4j+3 and 64+4j..64+4j+3, so
 // rotate_half pairs stay inside one lane. A 256-thread workgroup covers 16 head rows.
+#include <mutex>
+
 #include "common.h"
 
 namespace aspec {
@@ -307,6 +309,44 @@ int bwd_groups(const QkArgs& a) {
 }
 
 }  // namespace
+
+// Scratch of aspec_qk_norm_rope_bwd_noalloc: the per-workgroup weight-gradient partials of one
+// call, [2][groups][128] fp32 with groups <= kBwdMaxGroups, so 2 MiB covers every size. Each GPU
+// the library runs on holds its own copy until the process ends. Every slot a call reads is
+// written earlier in the same call, so nothing needs clearing between calls; calls that overlap
+// on one GPU share the array and race.
+static __device__ __align__(256) float scratch[2 * kBwdMaxGroups * kQkDim];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per device (no
+// allocation: the array is part of the loaded code object).
+int scratch_on_current_device(float** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess)
+    return set_error(ASPEC_ERR_RUNTIME, "hipGetDevice failed: %s", hipGetErrorString(err));
+  if (device < 0 || device >= kMaxScratchDevices)
+    return set_error(ASPEC_ERR_UNSUPPORTED, "device %d beyond the %d scratch slots", device,
+                     kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr)
+      return set_error(ASPEC_ERR_RUNTIME, "hipGetSymbolAddress(scratch) failed on device %d: %s",
+                       device, hipGetErrorString(err));
+    g_scratch_ptr[device] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[device];
+  return ASPEC_OK;
+}
+
+}  // namespace
 }  // namespace aspec
 
 using namespace aspec;
@@ -395,4 +435,30 @@ extern "C" int aspec_qk_norm_rope_bwd(
   if ((rc = check_launch("qk_norm_rope_bwd_kernel"))) return rc;
   hipLaunchKernelGGL(qk_norm_rope_dw_kernel, dim3(2 * kQkDim), dim3(256), 0, s, a, groups);
   return check_launch("qk_norm_rope_dw_kernel");
+}
+
+extern "C" int aspec_qk_norm_rope_bwd_noalloc(
+    const void* grad_q, const void* grad_k, const void* query, const void* context_key,
+    const void* draft_key, const float* rstd_q, const float* rstd_k, const void* q_weight,
+    const void* k_weight, const void* cos, const void* sin, int64_t rope_rows,
+    int64_t rope_stride, const int64_t* query_positions, const int64_t* context_positions,
+    const int64_t* draft_positions, int64_t batch, int64_t context_len, int64_t draft_len,
+    int64_t q_heads, int64_t kv_heads, int64_t head_dim, float eps, void* d_query,
+    void* d_context_key, void* d_draft_key, float* dw_q, float* dw_k, int32_t* status_flags,
+    void* stream) {
+  size_t need = 0;
+  int rc = aspec_qk_norm_rope_bwd_workspace_bytes(batch, context_len, draft_len, q_heads, kv_heads,
+                                                  &need);
+  if (rc) return rc;
+  if (need > sizeof(scratch))
+    return set_error(ASPEC_ERR_UNSUPPORTED,
+                     "Q/K norm+RoPE backward needs %zu bytes of scratch; the static scratch holds %zu",
+                     need, sizeof(scratch));
+  float* ptr = nullptr;
+  if ((rc = scratch_on_current_device(&ptr))) return rc;
+  return aspec_qk_norm_rope_bwd(grad_q, grad_k, query, context_key, draft_key, rstd_q, rstd_k,
+                                q_weight, k_weight, cos, sin, rope_rows, rope_stride,
+                                query_positions, context_positions, draft_positions, batch,
+                                context_len, draft_len, q_heads, kv_heads, head_dim, eps, d_query,
+                                d_context_key, d_draft_key, dw_q, dw_k, ptr, status_flags, stream);
 }

@@ -431,6 +431,28 @@ int aspec_qk_norm_rope_bwd(const void* grad_q, const void* grad_k, const void* q
                            void* workspace, int32_t* status_flags, void* stream);
 
 /*
+ * aspec_qk_norm_rope_bwd without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The weight-gradient partials live in a static 2 MiB device array
+ * that the library holds on each GPU it runs on until the process ends (every size fits: the
+ * kernel's grid is capped); its address is looked up on the first call on each device, with that
+ * device current. The entry point allocates nothing and calls no allocating routine. Calls that
+ * overlap on one GPU share the array and race: serialize them (one stream, or events).
+ */
+int aspec_qk_norm_rope_bwd_noalloc(const void* grad_q, const void* grad_k, const void* query,
+                                   const void* context_key, const void* draft_key,
+                                   const float* rstd_q, const float* rstd_k, const void* q_weight,
+                                   const void* k_weight, const void* cos, const void* sin,
+                                   int64_t rope_rows, int64_t rope_stride,
+                                   const int64_t* query_positions,
+                                   const int64_t* context_positions,
+                                   const int64_t* draft_positions, int64_t batch,
+                                   int64_t context_len, int64_t draft_len, int64_t q_heads,
+                                   int64_t kv_heads, int64_t head_dim, float eps, void* d_query,
+                                   void* d_context_key, void* d_draft_key, float* dw_q,
+                                   float* dw_k, int32_t* status_flags, void* stream);
+
+/*
  * RMSNorm forward over rows of `hidden` bf16 values (multiple of 8, at most 8192), with an
  * optional residual add: y = x + residual (bf16, written to y_out), rstd[r] = 1/sqrt(mean(y^2) +
  * eps), out = bf16(y * rstd * weight). Replaces `DFlashRMSNorm.forward` / `_dflash_rms_norm`
