@@ -350,15 +350,12 @@ struct ListWindow {
 // ---------------------------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
-                                         const bf16x8 (&qf)[8], f32x16 (&oacc)[4], float& m_run,
-                                         float& l_run, bool partial, const RowIntervals& iv, float scale_log2,
-                                         const TileOffsets& o, int g) {
-  f32x16 s[2];
-  mfma_chains2<kFwdAhead>(s[0], s[1], RowOperandT{sk, o}, RowOperandT{sk + 32 * kRowLd, o}, qf, qf);
-  bf16x8 vcur[4];
-#pragma unroll
-  for (int d = 0; d < 4; ++d) vcur[d] = read_tr_t(sv, o, 0, d);
+// Online softmax of one 64-key tile of scores S^T (`s`, lane = query row): masks a partial tile,
+// raises the running maximum (rescaling O and the row sum only when it grows by more than
+// kRescaleThreshold), and leaves P, rounded to bf16, in `pb` as the P.V operand.
+__device__ __forceinline__ void fwd_softmax(f32x16 (&s)[2], f32x16 (&oacc)[4], float& m_run,
+                                            float& l_run, bool partial, const RowIntervals& iv,
+                                            float scale_log2, int g, bf16x8 (&pb)[4]) {
   // Row maximum of the raw scores (scale > 0 commutes with max); the scale then folds into the
   // exponent: p = exp2(s * scale*log2e - m).
   if (partial) {
@@ -373,7 +370,7 @@ __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
 #pragma unroll
     for (int r = 0; r < 16; ++r) tile_max = fmaxf(tile_max, s[kb][r]);
   }
-  tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32)) * scale_log2;
+  tile_max = max_halves(tile_max) * scale_log2;
   const bool grow = tile_max > m_run + kRescaleThreshold;
   if (__any(grow)) {
     const float m_new = grow ? tile_max : m_run;
@@ -389,7 +386,6 @@ __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[kb][r] = fast_exp2(fmaf(s[kb][r], scale_log2, neg_m));
   }
-  bf16x8 pb[4];
   pb[0] = pack_c_half(s[0], 0);
   pb[1] = pack_c_half(s[0], 8);
   pb[2] = pack_c_half(s[1], 0);
@@ -397,6 +393,19 @@ __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
   // The row sum is taken over the rounded P that the P.V product uses, so O is normalized by
   // exactly the weights it was built from.
   l_run += sum_bf16(pb);
+}
+
+__device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
+                                         const bf16x8 (&qf)[8], f32x16 (&oacc)[4], float& m_run,
+                                         float& l_run, bool partial, const RowIntervals& iv, float scale_log2,
+                                         const TileOffsets& o, int g) {
+  f32x16 s[2];
+  mfma_chains2<kFwdAhead>(s[0], s[1], RowOperandT{sk, o}, RowOperandT{sk + 32 * kRowLd, o}, qf, qf);
+  bf16x8 vcur[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) vcur[d] = read_tr_t(sv, o, 0, d);
+  bf16x8 pb[4];
+  fwd_softmax(s, oacc, m_run, l_run, partial, iv, scale_log2, g, pb);
   mfma_tr_blocks_t<4>(oacc, sv, o, vcur, pb);
 }
 
@@ -668,9 +677,10 @@ struct KvStage {
 static_assert(offsetof(KvStage, delta) == offsetof(KvStage, lse2) + 4 * kBwdTileM, "layout");
 static_assert(offsetof(KvStage, ends) == offsetof(KvStage, delta) + 4 * kBwdTileM, "layout");
 
-// P of one iteration in C-register order: [slice][register quad][lane].
+// P of one iteration as the P wave's bf16 dV operand: [slice][C-register half][lane] (registers
+// 8h .. 8h+7 of the lane, two per 32-bit word, low half first).
 struct PExchange {
-  f32x4 p[kKvWaves][4][kWave];
+  uint4 p[kKvWaves][2][kWave];
 };
 
 // acc = A x B over the 128-dim reduction: A rows from LDS (all eight k-steps read up front), B
@@ -743,24 +753,29 @@ __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf1
         sacc[rq * 4 + j] = __int_as_float(__float_as_int(p) & keep);
       }
   }
-#pragma unroll
-  for (int rq = 0; rq < 4; ++rq)
-    px.p[w][rq][lane] = f32x4{sacc[rq * 4 + 0], sacc[rq * 4 + 1], sacc[rq * 4 + 2], sacc[rq * 4 + 3]};
   const bf16x8 pp[2] = {pack_c_half(sacc, 0), pack_c_half(sacc, 8)};
+  px.p[w][0][lane] = __builtin_bit_cast(uint4, pp[0]);
+  px.p[w][1][lane] = __builtin_bit_cast(uint4, pp[1]);
   mfma_tr_32(dvacc, s.dout, tro, pp);
 }
 
-// dS wave: dP, dS = P (dP - delta) and dK += dS^T Q for one stage.
+// dS wave: dP, dS = P (dP - delta) and dK += dS^T Q for one stage. P is the bf16 P the dV product
+// used (dS is rounded to bf16 for the dK product in any case).
 __device__ __forceinline__ void dkdv_ds_step(const KvStage& s, const PExchange& px,
                                              const bf16x8 (&vf)[8], f32x16 (&dkacc)[4], int w,
                                              const RowOffsets& ro, const TrOffsets& tro, int lane) {
   const int g = lane >> 5;
   f32x16 dp = mfma_chain_lds_reg(RowOperandR{s.dout, ro}, vf);
+  const uint4 ph[2] = {px.p[w][0][lane], px.p[w][1][lane]};
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq) {
     const int r0 = rq * 8 + g * 4;
     const f32x4 d4 = *reinterpret_cast<const f32x4*>(s.delta + r0);
-    const f32x4 p4 = px.p[w][rq][lane];
+    const uint4& h = ph[rq >> 1];
+    const uint32_t lo = (rq & 1) ? h.z : h.x;
+    const uint32_t hi = (rq & 1) ? h.w : h.y;
+    const f32x4 p4 = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u),
+                      __uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
 #pragma unroll
     for (int j = 0; j < 4; ++j) dp[rq * 4 + j] = p4[j] * (dp[rq * 4 + j] - d4[j]);
   }

@@ -155,6 +155,14 @@ struct RowIntervals {
   }
 };
 
+// max(x of this lane, x of lane ^ 32) with gfx950's v_permlane32_swap (no LDS round trip):
+// swapping lanes 32-63 of one copy with lanes 0-31 of another leaves each lane holding its own
+// value in one result and its partner's in the other.
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // The score of C register r, or -inf when its key is not visible (`w` from RowIntervals::word).
 __device__ __forceinline__ float masked_score(float s, uint32_t w, int r) {
   const int keep = __builtin_amdgcn_sbfe(static_cast<int>(w), (r >> 2) * 8 + (r & 3), 1);  // 0 or -1

@@ -283,8 +283,28 @@ def attention_configs(device, reps):
     return out
 
 
-def kernel_work(w, device):
-    """Algorithmic work per launch of each timed region (FLOPs for MFMA-bound, bytes for HBM-bound)."""
+def unique_teacher_rows(x):
+    """Distinct rows of the frozen-teacher table the step's indexed teacher reads (the DSpark
+    targets of the config's anchors, as `step` builds them)."""
+    import torch
+
+    from aspec_amd.anchors import validate_injected_anchors
+    from aspec_amd.targets import dspark_targets
+
+    w = x["w"]
+    anchors, keep, _, docs, _ = x["meta_tensors"]
+    anchors, keep = validate_injected_anchors(anchors, keep, loss_mask=x["loss_mask"],
+                                              num_anchors=w.num_blocks, block_size=w.block_size,
+                                              ctx_doc_ids=docs)
+    targets = dspark_targets(anchors, keep, x["input_ids"], x["loss_mask"], w.block_size,
+                             loss_decay_gamma=DECAY_GAMMA, ctx_doc_ids=docs)
+    return int(torch.unique(targets.teacher_index).numel())
+
+
+def kernel_work(w, device, teacher_rows):
+    """Algorithmic work per launch of each timed region (FLOPs for MFMA-bound, bytes for HBM-bound).
+    The loss kernels count each byte they must move once: the draft logits (and dlogits) of every
+    row, and the `teacher_rows` distinct rows of the indexed teacher table."""
     pairs = visible_pairs(w, device)
     hd = w.q_heads * w.head_dim
     rows, ctx = w.num_queries, w.context_length
@@ -296,8 +316,8 @@ def kernel_work(w, device):
         "head_gemm_fwd": ("mfma", 2 * rows * VOCAB * HIDDEN),
         "head_gemm_dgrad": ("mfma", 2 * rows * VOCAB * HIDDEN),
         "teacher_gemm": ("mfma", 2 * ctx * VOCAB * HIDDEN),
-        "loss_fwd": ("hbm", 2 * rows * VOCAB * 2),
-        "loss_bwd": ("hbm", 3 * rows * VOCAB * 2),
+        "loss_fwd": ("hbm", (rows + teacher_rows) * VOCAB * 2),
+        "loss_bwd": ("hbm", (2 * rows + teacher_rows) * VOCAB * 2),
         "thd_row_metadata": ("hbm", w.num_blocks * 17 + ctx * 16 + rows * 4 * 4 + w.num_keys * 4 * 4 + rows * 5 * 4),
         "attn_plan_build": ("hbm", rows * 5 * 4 * 2),
         # anchors + keep in, masked anchors out, two loss-mask and two doc reads per kept anchor
@@ -727,7 +747,10 @@ def main():
         kernels = _timing.summary()
         set_backward_overlap(overlap)
 
-    pairs, work = kernel_work(w, device)
+    teacher_rows = unique_teacher_rows(x)
+    pairs, work = kernel_work(w, device, teacher_rows)
+    # the loss bytes as the per-row accounting states them (every row reads a full teacher row)
+    survey_bytes = {"loss_fwd": 2 * w.num_queries * VOCAB * 2, "loss_bwd": 3 * w.num_queries * VOCAB * 2}
     per_kernel = {}
     for name, stats in kernels.items():
         bound, amount = work.get(name, (None, None))
@@ -737,7 +760,11 @@ def main():
             entry.update(tflops=round(tf, 2), frac_mfma=round(tf / PEAK_BF16_TFLOPS, 4))
         elif bound == "hbm":
             gbs = amount / (stats["mean_ms"] * 1e-3) / 1e9
-            entry.update(gbs=round(gbs, 1), frac_hbm=round(gbs / PEAK_HBM_GBS, 4))
+            entry.update(gbs=round(gbs, 1), frac_hbm=round(gbs / PEAK_HBM_GBS, 4), bytes=amount)
+            if name in survey_bytes:
+                sgbs = survey_bytes[name] / (stats["mean_ms"] * 1e-3) / 1e9
+                entry.update(teacher_rows=teacher_rows, per_row_bytes=survey_bytes[name],
+                             per_row_frac_hbm=round(sgbs / PEAK_HBM_GBS, 4))
         per_kernel[name] = entry
     if not args.no_kernel_timing:
         aux = dict(aux_rows(device, w, args.steps))
