@@ -63,6 +63,41 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// All-lane reductions of a wave in registers (no LDS): DPP quad permutes and row mirrors combine
+// the 16 lanes of each row (after xor 1 and xor 2 every quad is uniform, so the half mirror and
+// the mirror each add an equal partner group), then v_permlane16_swap and v_permlane32_swap
+// combine the rows pairwise: swapping the odd rows (halves) of one copy with the even rows
+// (halves) of another leaves each lane holding its own value in one result and its partner's in
+// the other.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_allreduce_bits(uint32_t v, Op op) {
+  v = op(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = op(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = op(v, dpp_u32<0x141>(v));  // row_half_mirror
+  v = op(v, dpp_u32<0x140>(v));  // row_mirror
+  const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = op(r16[0], r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return op(r32[0], r32[1]);
+}
+__device__ __forceinline__ float wave_allsum(float v) {
+  return __uint_as_float(wave_allreduce_bits(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+    return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  }));
+}
+__device__ __forceinline__ float wave_allmax(float v) {  // a NaN operand is skipped, as fmaxf does
+  return __uint_as_float(wave_allreduce_bits(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }));
+}
+__device__ __forceinline__ uint32_t wave_allmin(uint32_t v) {
+  return wave_allreduce_bits(v, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
   return v;

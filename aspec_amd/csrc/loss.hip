@@ -79,6 +79,19 @@ __device__ __forceinline__ int64_t teacher_row(const LossArgs& a, int64_t row) {
 
 __device__ __forceinline__ float bf(uint16_t v) { return bf16_to_f32(v); }
 
+// Wave-uniform reads of kernel inputs through the scalar cache (constant address space): they
+// are counted by lgkmcnt, so no wait for them also waits for the vector loads in flight.
+template <typename T>
+__device__ __forceinline__ T scalar_read(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)(p);
+}
+// The bf16 at p (wave-uniform address), read as its aligned 32-bit word.
+__device__ __forceinline__ float scalar_read_bf16(const uint16_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t w = scalar_read(reinterpret_cast<const uint32_t*>(a & ~static_cast<uintptr_t>(3)));
+  return __uint_as_float((a & 2) ? (w & 0xffff0000u) : (w << 16));
+}
+
 // Masses of p against q: accumulates |p-q| and p split by sign(p-q) (tiled_l1.py:76-92).
 __device__ __forceinline__ void l1_terms(float p, float q, float& l1, float& pos, float& neg, float& zero) {
   l1 += fabsf(p - q);
@@ -135,6 +148,8 @@ __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w <<
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 constexpr int kWalkThreads = 512;  // threads of the persistent row walk (8 waves, 2 per SIMD)
+// Eight bf16 -inf: what the row walk's lanes past the end of a row load.
+__device__ const uint4 kNegInfChunk = {0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u};
 constexpr int kWalkWaves = kWalkThreads / 64;
 
 // Per-thread max and exp2 values of NV chunks of eight bf16 logits (chunk j of thread t holds
@@ -149,9 +164,23 @@ __device__ __forceinline__ float max3_raw(float a, float b, float c) {
   return r;
 }
 
-template <int NV>
+// min(a, |b|) as one v_min_f32 with an absolute-value source modifier (fminf would first quiet
+// both operands).
+__device__ __forceinline__ float min_abs_raw(float a, float b) {
+  float r;
+  asm("v_min_f32_e64 %0, %1, |%2|" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+struct NoChunkHook {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+
+// `after_chunk(j)` runs once chunk j's exponentials are computed (the row walk issues a load of
+// the next row there, so the loads enter the memory pipeline between VALU work).
+template <int NV, typename Hook = NoChunkHook>
 __device__ __forceinline__ void chunk_exps(const uint4 (&v)[NV], float (&e)[NV * 8], float& m,
-                                           float& sum) {
+                                           float& sum, const Hook& after_chunk = Hook{}) {
   m = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -170,16 +199,28 @@ __device__ __forceinline__ void chunk_exps(const uint4 (&v)[NV], float (&e)[NV *
       e[j * 8 + 2 * k + 1] = scaled_exp2(hi_bf(w[k]), nm);
       sum += e[j * 8 + 2 * k] + e[j * 8 + 2 * k + 1];
     }
+    after_chunk(j);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-// Merges every thread's (max, sum) pair for NP quantities; `slots` holds 2*NP*kWalkWaves floats.
+// A (max, sum) pair's sum relative to `to` (>= its max): a pair whose max is -inf passes its sum
+// (0, or NaN from a NaN logit) unscaled; a +inf max against a +inf `to` gives NaN, as softmax
+// does.
+__device__ __forceinline__ float sum_relative_to(float m, float s, float to) {
+  return m == -INFINITY ? s : s * fexp2((m - to) * kLog2e);
+}
+
+// Merges every thread's (max, sum) pair for NP quantities: within each wave in registers, then
+// across the waves through `slots` (2*NP*kWalkWaves floats, one barrier).
 template <int NP>
 __device__ __forceinline__ void block_merge(float (&m)[NP], float (&sm)[NP], float* slots) {
 #pragma unroll
-  for (int i = 0; i < NP; ++i)
-    for (int off = 32; off > 0; off >>= 1)
-      merge_max_sum(m[i], sm[i], __shfl_xor(m[i], off), __shfl_xor(sm[i], off));
+  for (int i = 0; i < NP; ++i) {
+    const float mw = wave_allmax(m[i]);
+    sm[i] = wave_allsum(sum_relative_to(m[i], sm[i], mw));
+    m[i] = mw;
+  }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
 #pragma unroll
@@ -191,10 +232,13 @@ __device__ __forceinline__ void block_merge(float (&m)[NP], float (&sm)[NP], flo
   lds_barrier();
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
-    float mm = slots[(2 * i) * kWalkWaves], ss = slots[(2 * i + 1) * kWalkWaves];
+    float mm = slots[(2 * i) * kWalkWaves];
 #pragma unroll
-    for (int w = 1; w < kWalkWaves; ++w)
-      merge_max_sum(mm, ss, slots[(2 * i) * kWalkWaves + w], slots[(2 * i + 1) * kWalkWaves + w]);
+    for (int w = 1; w < kWalkWaves; ++w) mm = fmaxf(mm, slots[(2 * i) * kWalkWaves + w]);
+    float ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWalkWaves; ++w)
+      ss += sum_relative_to(slots[(2 * i) * kWalkWaves + w], slots[(2 * i + 1) * kWalkWaves + w], mm);
     m[i] = mm;
     sm[i] = mm == -INFINITY ? NAN : ss;  // a row of -inf (or padding only): NaN, as torch gives
   }
@@ -213,9 +257,8 @@ template <int NP>
 __device__ __forceinline__ void block_sums(float (&v)[NP], uint32_t& key, float* slots,
                                            uint32_t* key_slots) {
 #pragma unroll
-  for (int i = 0; i < NP; ++i)
-    for (int off = 32; off > 0; off >>= 1) v[i] += __shfl_xor(v[i], off);
-  for (int off = 32; off > 0; off >>= 1) key = min(key, static_cast<uint32_t>(__shfl_xor(static_cast<int>(key), off)));
+  for (int i = 0; i < NP; ++i) v[i] = wave_allsum(v[i]);
+  key = wave_allmin(key);
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
 #pragma unroll
@@ -235,7 +278,7 @@ __device__ __forceinline__ void block_sums(float (&v)[NP], uint32_t& key, float*
   for (int w = 1; w < kWalkWaves; ++w) key = min(key, key_slots[w]);
 }
 
-template <int NV, bool ARGMAX>
+template <int NV, bool ARGMAX, bool HAS_Y>
 __global__ void __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 loss_fwd_persistent(LossArgs args) {
   __shared__ float merge_slots[4 * kWalkWaves];  // (max, sum) of x and y per wave
@@ -256,23 +299,25 @@ loss_fwd_persistent(LossArgs args) {
   int32_t* const flags = args.flags;
   int64_t* const amax_out = args.amax;
   const int tid = threadIdx.x;
-  const bool has_y = ybase != nullptr;
+  constexpr bool has_y = HAS_Y;  // a compile-time teacher: every path issues the same loads
   const uint32_t nchunks = static_cast<uint32_t>(V / 8);
-  const uint4 ninf = make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u);  // -inf
   uint4 nx[NV], ny[NV];
-  auto fetch = [&](int64_t r, int64_t tr) {
-    const uint4* xq = reinterpret_cast<const uint4*>(xbase + r * V);
-    const uint4* yq = has_y && tr >= 0 ? reinterpret_cast<const uint4*>(ybase + tr * V) : nullptr;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const uint32_t chunk = j * static_cast<uint32_t>(kWalkThreads) + tid;
-      nx[j] = ninf;
-      ny[j] = ninf;
-      if (chunk < nchunks) {
-        nx[j] = xq[chunk];
-        if (yq) ny[j] = yq[chunk];
-      }
-    }
+  // Chunk j of a row (j * kWalkThreads + tid). Every lane loads: a lane past the row's end reads
+  // the -inf chunk, a teacher row out of range reads row 0 (its loss is NaN), and the last row of
+  // a workgroup re-reads itself as its "next" row. NV is the smallest size that covers V, so only
+  // chunks j >= NV/2 can reach past the row's end.
+  // (global address space throughout: a select with a generic pointer would make these flat
+  // loads, which LDS waits and barriers then also wait for)
+  typedef const __attribute__((address_space(1))) uint4* GlobalChunk;
+  auto src = [&](const uint16_t* row_base, int j) __attribute__((always_inline)) {
+    const uint32_t chunk = static_cast<uint32_t>(j) * static_cast<uint32_t>(kWalkThreads) + tid;
+    GlobalChunk p = (GlobalChunk)(row_base) + chunk;
+    if (NV == 2 || j >= NV / 2) p = chunk < nchunks ? p : (GlobalChunk)(&kNegInfChunk);
+    return (const uint4*)p;
+  };
+  auto load_x = [&](int j, int64_t r) __attribute__((always_inline)) { nx[j] = *src(xbase + r * V, j); };
+  auto load_y = [&](int j, int64_t tr) __attribute__((always_inline)) {
+    ny[j] = *src(ybase + (tr >= 0 && tr < trows ? tr : 0) * V, j);
   };
   auto teacher = [&](int64_t r) -> int64_t {  // teacher row of draft row r, -1 when out of range
     if (!has_y) return 0;
@@ -288,32 +333,37 @@ loss_fwd_persistent(LossArgs args) {
   if (row >= rows) return;
   int64_t trow = teacher(row);
   int64_t tgt = ce_out ? target[row] : ignore;
-  fetch(row, trow);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) load_x(j, row);
+  if (has_y) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) load_y(j, trow);
+  }
   while (row < rows) {
-    // the next row's index and target, loaded while this row is computed
+    // The next row's teacher index and target: loaded here, first used after the next row's draft
+    // logits have been requested (so waiting for them waits for nothing else).
     const int64_t next = row + gridDim.x;
-    int64_t trow_n = 0, tgt_n = ignore;
-    if (next < rows) {
-      trow_n = teacher(next);
-      tgt_n = ce_out ? target[next] : ignore;
-    }
-    // the CE target logit (thread 0, from L2: the row has just been read)
+    const int64_t nsafe = next < rows ? next : row;
+    const int64_t tidx_n = has_y && yidx ? scalar_read(yidx + nsafe) : nsafe;
+    const int64_t tgt_n = ce_out ? scalar_read(target + nsafe) : ignore;
+    // the CE target logit (from cache: the row has just been read)
     const bool tgt_ok = tgt != ignore && tgt >= 0 && tgt < V;
-    float target_logit = 0.f;
-    if (tid == 0 && tgt_ok) target_logit = bf(xbase[row * V + tgt]);
+    const float target_logit = tgt_ok ? scalar_read_bf16(xbase + row * V + tgt) : 0.f;
     float ex[NV * 8], ey[NV * 8];
     float m[2], sm[2];
     chunk_exps<NV>(nx, ex, m[0], sm[0]);
     m[1] = -INFINITY;
     sm[1] = 0.f;
-    if (has_y) chunk_exps(ny, ey, m[1], sm[1]);
-    // The target logit and the next row's index have arrived before the next row's loads go out,
-    // so no later wait for them also waits for those loads. The loads stay below the last read of
-    // this row's packed registers, which they reuse.
-    asm volatile("" ::"v"(target_logit), "v"(trow_n), "v"(tgt_n));
-    __builtin_amdgcn_sched_barrier(0);
-    if (next < rows) fetch(next, trow_n);
-    const float mx_local = m[0], my_local = m[1];
+    // The next row's draft logits stream in while the teacher's exponentials are computed (one
+    // chunk per step, into the registers chunk_exps has just consumed), its teacher logits during
+    // the L1 masses below.
+    if (has_y) {
+      chunk_exps<NV>(ny, ey, m[1], sm[1], [&](int j) __attribute__((always_inline)) { load_x(j, nsafe); });
+    } else {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) load_x(j, nsafe);
+    }
+    const float mx_local = m[0], my_local = m[1], sx_local = sm[0];
     block_merge<2>(m, sm, merge_slots);
     uint32_t key = kNoKey;
     if (ARGMAX) {
@@ -341,15 +391,54 @@ loss_fwd_persistent(LossArgs args) {
     const float cx = (mx_local == -INFINITY ? 0.f : fexp2((mx_local - m[0]) * kLog2e)) / sm[0];
     const float cy = (my_local == -INFINITY ? 0.f : fexp2((my_local - m[1]) * kLog2e)) / sm[1];
     float acc[4] = {0.f, 0.f, 0.f, 0.f};  // |p-q|, mass p>q, mass p<q, sum p
+    int64_t trow_n = 0;
     if (has_y) {
-#pragma unroll
-      for (int i = 0; i < NV * 8; ++i) {
-        const float pv = ex[i] * cx, qv = ey[i] * cy;
-        acc[0] += fabsf(pv - qv);
-        acc[1] += pv > qv ? pv : 0.f;
-        acc[2] += pv < qv ? pv : 0.f;
-        acc[3] += pv;
+      trow_n = tidx_n;
+      if (yidx && next < rows && (trow_n < 0 || trow_n >= trows)) {
+        if (tid == 0) atomicOr(flags, 1);
+        trow_n = -1;
       }
+      // Every chunk but the last (the only one that can reach past the row's end): |p - q| and,
+      // unless the chunk holds an exact tie, the signed mass S = sum copysign(p, p - q), seven VALU
+      // operations per element; then, with T = sum p over those chunks, mass(p > q) = (T + S) / 2
+      // and mass(p < q) = (T - S) / 2. A chunk with a tie (identical rows, both logits masked)
+      // and the last chunk count their masses element by element, so ties keep their own mass
+      // exactly (identical rows give exactly zero masses and gradient).
+      float sgn = 0.f, exact_sum = 0.f;
+      bool any_fast = false;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        float pj[8], dj[8];
+        float mj = INFINITY;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          pj[k] = ex[j * 8 + k] * cx;
+          dj[k] = pj[k] - ey[j * 8 + k] * cy;
+          acc[0] += fabsf(dj[k]);
+          mj = min_abs_raw(mj, dj[k]);
+        }
+        if (j < NV - 1 && mj != 0.f) {
+          any_fast = true;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) sgn += copysignf(pj[k], dj[k]);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            acc[1] += dj[k] > 0.f ? pj[k] : 0.f;
+            acc[2] += dj[k] < 0.f ? pj[k] : 0.f;
+            exact_sum += pj[k];
+          }
+        }
+        load_y(j, trow_n);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const float total = cx * sx_local;
+      if (any_fast) {
+        const float t = total - exact_sum;
+        acc[1] += 0.5f * (t + sgn);
+        acc[2] += 0.5f * (t - sgn);
+      }
+      acc[3] = total;
     }
     block_sums<4>(acc, key, sum_slots, key_slots);
     if (tid == 0) {
@@ -504,6 +593,17 @@ __global__ void __launch_bounds__(256) loss_bwd_kernel(LossArgs a) {
   }
 }
 
+template <int NV>
+void launch_walk(const LossArgs& a, dim3 walk, dim3 block, hipStream_t s) {
+  if (a.y) {
+    if (a.amax) hipLaunchKernelGGL((loss_fwd_persistent<NV, true, true>), walk, block, 0, s, a);
+    else hipLaunchKernelGGL((loss_fwd_persistent<NV, false, true>), walk, block, 0, s, a);
+  } else {
+    if (a.amax) hipLaunchKernelGGL((loss_fwd_persistent<NV, true, false>), walk, block, 0, s, a);
+    else hipLaunchKernelGGL((loss_fwd_persistent<NV, false, false>), walk, block, 0, s, a);
+  }
+}
+
 int launch_fwd(const LossArgs& a, hipStream_t s) {
   const bool vec = a.V % 8 == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
                    (!a.y || (reinterpret_cast<uintptr_t>(a.y) & 15) == 0);
@@ -515,14 +615,11 @@ int launch_fwd(const LossArgs& a, hipStream_t s) {
   const dim3 walk(static_cast<uint32_t>(std::min<int64_t>(a.rows, cus)));
   const dim3 block(kWalkThreads);
   if (vec && a.V <= kWalkThreads * 8 * 2) {
-    if (a.amax) hipLaunchKernelGGL((loss_fwd_persistent<2, true>), walk, block, 0, s, a);
-    else hipLaunchKernelGGL((loss_fwd_persistent<2, false>), walk, block, 0, s, a);
+    launch_walk<2>(a, walk, block, s);
   } else if (vec && a.V <= kWalkThreads * 8 * 4) {
-    if (a.amax) hipLaunchKernelGGL((loss_fwd_persistent<4, true>), walk, block, 0, s, a);
-    else hipLaunchKernelGGL((loss_fwd_persistent<4, false>), walk, block, 0, s, a);
+    launch_walk<4>(a, walk, block, s);
   } else if (vec && a.V <= kWalkThreads * 8 * 8) {
-    if (a.amax) hipLaunchKernelGGL((loss_fwd_persistent<8, true>), walk, block, 0, s, a);
-    else hipLaunchKernelGGL((loss_fwd_persistent<8, false>), walk, block, 0, s, a);
+    launch_walk<8>(a, walk, block, s);
   } else {
     hipLaunchKernelGGL(loss_fwd_streaming, grid, dim3(256), 0, s, a);
   }
