@@ -544,6 +544,84 @@ __device__ __forceinline__ float grad_elem(float x, float y, const float* st, fl
   return d;
 }
 
+// Vectorised path (V % 8 == 0): each workgroup pass covers 256 consecutive chunks of eight logits
+// of one row, so the row's statistics, upstream gradients, target and teacher index are
+// wave-uniform and read through the scalar cache; only the logits and dx use the vector memory
+// path.
+constexpr int kBwdThreads = 256;
+
+__global__ void __launch_bounds__(kBwdThreads) loss_bwd_rows_kernel(LossArgs a) {
+  const int64_t per_row = a.V / 8;
+  const int64_t segs_per_row = (per_row + kBwdThreads - 1) / kBwdThreads;
+  const int64_t segs = a.rows * segs_per_row;
+  const bool has_y = a.y != nullptr;
+  for (int64_t seg = blockIdx.x; seg < segs; seg += gridDim.x) {
+    const int64_t row = seg / segs_per_row;
+    const int64_t chunk = (seg - row * segs_per_row) * kBwdThreads + threadIdx.x;
+    float st[kStats];
+#pragma unroll
+    for (int i = 0; i < kStats; ++i) st[i] = scalar_read(a.stats + row * kStats + i);
+    const float gl1 = (has_y && a.g_l1) ? scalar_read(a.g_l1 + row) : 0.f;
+    float gce = 0.f;
+    int64_t tgt = -1;
+    if (a.g_ce) {
+      tgt = scalar_read(a.target + row);
+      gce = tgt == a.ignore_index ? 0.f : scalar_read(a.g_ce + row);
+    }
+    int64_t trow = 0;
+    if (has_y) {
+      trow = a.yidx ? scalar_read(a.yidx + row) : row;
+      if (trow < 0 || trow >= a.trows) trow = -1;
+    }
+    if (chunk >= per_row) continue;
+    // dx = p * (L1 weight of the element's case + g_ce) - g_ce at the target, p = e_x / S_x with
+    // e = exp2(v log2e - max log2e) (scaled_exp2, as grad_elem). Per row: the three case weights
+    // times 1/S_x, and r = (1/S_y) / (1/S_x), so p against q is e_x against e_y * r (identical rows:
+    // r = 1 and e_x == e_y, the p == q case).
+    const float nmx = neg_scaled_max(st[0]), nmy = neg_scaled_max(st[2]);
+    const float pos = st[4], neg = st[5], zero = st[6];
+    const float k_gt = st[1] * ((2.f * neg + zero) * gl1 + gce);
+    const float k_lt = st[1] * ((-2.f * pos - zero) * gl1 + gce);
+    const float k_eq = st[1] * ((neg - pos) * gl1 + gce);
+    const float k_ce = st[1] * gce;  // no teacher: the CE part alone
+    const float r = st[3] / st[1];
+    const int64_t col0 = chunk * 8;
+    const uint16_t* xr = a.x + row * a.V;
+    const uint16_t* yr = (has_y && trow >= 0) ? a.y + trow * a.V : nullptr;
+    const uint4 xs = *reinterpret_cast<const uint4*>(xr + col0);
+    const uint4 ys = yr ? *reinterpret_cast<const uint4*>(yr + col0) : make_uint4(0, 0, 0, 0);
+    const uint32_t xw[4] = {xs.x, xs.y, xs.z, xs.w};
+    const uint32_t yw[4] = {ys.x, ys.y, ys.z, ys.w};
+    float d[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = (e & 1) ? __uint_as_float(xw[e >> 1] & 0xffff0000u) : __uint_as_float(xw[e >> 1] << 16);
+      const float ex = scaled_exp2(x, nmx);
+      float k = k_ce;
+      if (has_y) {
+        if (yr) {
+          const float y = (e & 1) ? __uint_as_float(yw[e >> 1] & 0xffff0000u) : __uint_as_float(yw[e >> 1] << 16);
+          const float qs = scaled_exp2(y, nmy) * r;
+          k = ex > qs ? k_gt : (ex < qs ? k_lt : k_eq);
+        } else {
+          k = NAN;  // teacher row out of range: NaN, as grad_elem gives
+        }
+      }
+      d[e] = ex * k;
+    }
+    // the CE target column (one lane of the row)
+    if (gce != 0.f && tgt >= col0 && tgt < col0 + 8) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (col0 + e == tgt) d[e] -= gce;
+    }
+    uint32_t out[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = pack_bf16x2(d[2 * e], d[2 * e + 1]);
+    *reinterpret_cast<uint4*>(a.dx + row * a.V + col0) = make_uint4(out[0], out[1], out[2], out[3]);
+  }
+}
+
 template <bool VEC>
 __global__ void __launch_bounds__(256) loss_bwd_kernel(LossArgs a) {
   const int64_t per_row = VEC ? a.V / 8 : a.V;
@@ -633,7 +711,9 @@ int launch_bwd(const LossArgs& a, hipStream_t s) {
   const int64_t work = a.rows * (vec ? a.V / 8 : a.V);
   const int64_t blocks = std::min<int64_t>((work + 255) / 256, 256 * 64);
   if (vec) {
-    hipLaunchKernelGGL(loss_bwd_kernel<true>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, s, a);
+    const int64_t segs = a.rows * ((a.V / 8 + kBwdThreads - 1) / kBwdThreads);
+    const int64_t grid = std::min<int64_t>(segs, 256 * 64);
+    hipLaunchKernelGGL(loss_bwd_rows_kernel, dim3(static_cast<uint32_t>(grid)), dim3(kBwdThreads), 0, s, a);
   } else {
     hipLaunchKernelGGL(loss_bwd_kernel<false>, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, s, a);
   }
