@@ -332,7 +332,7 @@ def kernel_work(w, device, teacher_rows):
 # the head GEMMs are the library kernels the recorded TunableOp solutions select
 _REGION_KERNEL = {"attn_fwd": "attn_fwd_kernel<4>", "attn_bwd_dq": "attn_bwd_dq_kernel<4>",
                   "attn_bwd_dkdv": "attn_bwd_dkdv_kernel<4>", "attn_bwd_prepare": "attn_bwd_pre_kernel",
-                  "loss_fwd": "loss_fwd_persistent<8, false>", "loss_bwd": "loss_bwd_kernel<true>",
+                  "loss_fwd": "loss_fwd_persistent<8, false, true>", "loss_bwd": "loss_bwd_rows_kernel",
                   "head_gemm_fwd": "Custom_Cijk_Alik_Bljk_BBS_BH_MT256x256x64_MI16x16x1_UserArgs_shortname0_gfx950",
                   "qk_norm_rope_fwd": "qk_norm_rope_fwd_kernel", "qk_norm_rope_bwd": "qk_norm_rope_bwd_kernel"}
 _LIBRARY_REGIONS = ("head_gemm_fwd", "head_gemm_dgrad", "teacher_gemm")
