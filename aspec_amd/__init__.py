@@ -56,6 +56,8 @@ from aspec_amd.output_blocks import (  # noqa: F401
     restore_blocks,
     select_blocks,
 )
+from aspec_amd.head_loss import selective_head_objective  # noqa: F401
+from aspec_amd.loss import ce_l1_fused_grad  # noqa: F401
 from aspec_amd.thd_attention import thd_fa4_attention  # noqa: F401
 from aspec_amd.thd_sparse_metadata import build_thd_sparse_pair  # noqa: F401
 from aspec_amd.tiled_l1 import tiled_l1_from_logits  # noqa: F401

@@ -66,6 +66,9 @@ SIGNATURES = {
     "aspec_ce_l1_bwd": (
         _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64] + [_c_void_p] * 5
     ),
+    "aspec_ce_l1_fused_fwd_bwd": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64] + [_c_void_p] * 9
+    ),
     "aspec_pack_copy": (_int, [_c_void_p, _i64, _c_void_p]),
     "aspec_pack_row_metadata": (_int, [_c_void_p, _i64, _i64] + [_c_void_p] * 4),
     "aspec_sample_document_anchors": (
@@ -110,7 +113,7 @@ SIGNATURES = {
     "aspec_pack_work_aware_rows": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib = None

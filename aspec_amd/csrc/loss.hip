@@ -278,9 +278,14 @@ __device__ __forceinline__ void block_sums(float (&v)[NP], uint32_t& key, float*
   for (int w = 1; w < kWalkWaves; ++w) key = min(key, key_slots[w]);
 }
 
-template <int NV, bool ARGMAX, bool HAS_Y>
+// GRAD (with a teacher only): once a row's statistics are final, the walk also writes the row's
+// dlogits for the objective sum_r (g_ce[r] ce[r] + g_l1[r] l1[r]) from the p and q it still holds,
+// dx = p * (L1 case weight * g_l1 + g_ce) - g_ce at the target (the backward's formula), into `dx`
+// (which may be the logits themselves: the row has been read by then).
+template <int NV, bool ARGMAX, bool HAS_Y, bool GRAD = false>
 __global__ void __launch_bounds__(kWalkThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 loss_fwd_persistent(LossArgs args) {
+  static_assert(!GRAD || HAS_Y, "the fused gradient needs a teacher");
   __shared__ float merge_slots[4 * kWalkWaves];  // (max, sum) of x and y per wave
   __shared__ float sum_slots[4 * kWalkWaves];    // |p-q|, p>q, p<q masses and sum p per wave
   __shared__ uint32_t key_slots[kWalkWaves];      // argmax key per wave
@@ -429,7 +434,7 @@ loss_fwd_persistent(LossArgs args) {
             exact_sum += pj[k];
           }
         }
-        load_y(j, trow_n);
+        if constexpr (!GRAD) load_y(j, trow_n);  // GRAD: after this chunk's dlogits (below)
         __builtin_amdgcn_sched_barrier(0);
       }
       const float total = cx * sx_local;
@@ -441,6 +446,48 @@ loss_fwd_persistent(LossArgs args) {
       acc[3] = total;
     }
     block_sums<4>(acc, key, sum_slots, key_slots);
+    if constexpr (GRAD) {
+      // the row's objective weights (wave-uniform) and the three L1 case weights (the backward's
+      // centered terms, tiled_l1.py:107-127)
+      const float wl1 = trow >= 0 ? scalar_read(args.g_l1 + row) : NAN;
+      const float wce = tgt != ignore ? scalar_read(args.g_ce + row) : 0.f;
+      const float pos = acc[1], neg = acc[2], zero = acc[3] - acc[1] - acc[2];
+      const float k_gt = (2.f * neg + zero) * wl1 + wce;
+      const float k_lt = (-2.f * pos - zero) * wl1 + wce;
+      const float k_eq = (neg - pos) * wl1 + wce;
+      uint16_t* const drow = args.dx + row * V;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const uint32_t chunk = static_cast<uint32_t>(j) * static_cast<uint32_t>(kWalkThreads) + tid;
+        float d[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float pv = ex[j * 8 + k] * cx, qv = ey[j * 8 + k] * cy;
+          d[k] = pv * (pv > qv ? k_gt : (pv < qv ? k_lt : k_eq));
+        }
+        // the CE target: chunk tgt / 8 belongs to thread (tgt / 8) % kWalkThreads at step
+        // (tgt / 8) / kWalkThreads (all wave-uniform but the thread)
+        if (tgt_ok && (tgt >> 3) / kWalkThreads == j && static_cast<int64_t>(tid) == (tgt >> 3) % kWalkThreads) {
+          switch (static_cast<int>(tgt & 7)) {
+            case 0: d[0] -= wce; break;
+            case 1: d[1] -= wce; break;
+            case 2: d[2] -= wce; break;
+            case 3: d[3] -= wce; break;
+            case 4: d[4] -= wce; break;
+            case 5: d[5] -= wce; break;
+            case 6: d[6] -= wce; break;
+            default: d[7] -= wce; break;
+          }
+        }
+        if (chunk < nchunks)
+          reinterpret_cast<uint4*>(drow)[chunk] =
+              make_uint4(pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3]), pack_bf16x2(d[4], d[5]),
+                         pack_bf16x2(d[6], d[7]));
+        // the next row's teacher chunk, into registers this row no longer needs
+        load_y(j, trow_n);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
     if (tid == 0) {
       if (ARGMAX) amax_out[row] = static_cast<int64_t>(key & 0x7fffffffu);
       const float lse = logf(sm[0]) + m[0];
@@ -673,6 +720,11 @@ __global__ void __launch_bounds__(256) loss_bwd_kernel(LossArgs a) {
 
 template <int NV>
 void launch_walk(const LossArgs& a, dim3 walk, dim3 block, hipStream_t s) {
+  if (a.dx) {  // the fused forward + dlogits (teacher present, checked by the entry point)
+    if (a.amax) hipLaunchKernelGGL((loss_fwd_persistent<NV, true, true, true>), walk, block, 0, s, a);
+    else hipLaunchKernelGGL((loss_fwd_persistent<NV, false, true, true>), walk, block, 0, s, a);
+    return;
+  }
   if (a.y) {
     if (a.amax) hipLaunchKernelGGL((loss_fwd_persistent<NV, true, true>), walk, block, 0, s, a);
     else hipLaunchKernelGGL((loss_fwd_persistent<NV, false, true>), walk, block, 0, s, a);
@@ -692,6 +744,9 @@ int launch_fwd(const LossArgs& a, hipStream_t s) {
     return set_error(ASPEC_ERR_RUNTIME, "cannot query the GPU's compute-unit count");
   const dim3 walk(static_cast<uint32_t>(std::min<int64_t>(a.rows, cus)));
   const dim3 block(kWalkThreads);
+  if (a.dx && !(vec && a.V <= kWalkThreads * 8 * 8 && (reinterpret_cast<uintptr_t>(a.dx) & 15) == 0))
+    return set_error(ASPEC_ERR_UNSUPPORTED, "the fused loss forward + dlogits needs V %% 8 == 0, V <= %d "
+                     "and 16-byte aligned rows", kWalkThreads * 8 * 8);
   if (vec && a.V <= kWalkThreads * 8 * 2) {
     launch_walk<2>(a, walk, block, s);
   } else if (vec && a.V <= kWalkThreads * 8 * 4) {
@@ -760,6 +815,41 @@ extern "C" int aspec_ce_l1_argmax_fwd(const void* logits, const void* teacher,
   a.amax = argmax_out;
   if (argmax_out && vocab > 0x7fffffffLL)
     return set_error(ASPEC_ERR_UNSUPPORTED, "argmax needs a vocabulary below 2^31");
+  return launch_fwd(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int aspec_ce_l1_fused_fwd_bwd(const void* logits, const void* teacher,
+                                          const int64_t* teacher_index, int64_t teacher_rows,
+                                          const int64_t* targets, int64_t ignore_index, int64_t rows,
+                                          int64_t vocab, const float* grad_ce, const float* grad_l1,
+                                          float* l1_out, float* ce_out, int64_t* argmax_out,
+                                          float* stats, void* grad_logits, int32_t* status_flags,
+                                          void* stream) {
+  int rc = check_common(rows, vocab, logits);
+  if (rc) return rc;
+  if (!teacher || !targets || !grad_ce || !grad_l1 || !grad_logits || !stats || !status_flags || !l1_out || !ce_out)
+    return set_error(ASPEC_ERR_INVALID, "the fused loss needs teacher logits, targets, both per-row "
+                     "gradients, outputs, stats, a status buffer and a dlogits buffer");
+  if (teacher_index && teacher_rows <= 0) return set_error(ASPEC_ERR_INVALID, "indexed teacher table is empty");
+  if (argmax_out && vocab > 0x7fffffffLL)
+    return set_error(ASPEC_ERR_UNSUPPORTED, "argmax needs a vocabulary below 2^31");
+  LossArgs a = {};
+  a.x = static_cast<const uint16_t*>(logits);
+  a.y = static_cast<const uint16_t*>(teacher);
+  a.yidx = teacher_index;
+  a.trows = teacher_index ? teacher_rows : rows;
+  a.target = targets;
+  a.ignore_index = ignore_index;
+  a.rows = rows;
+  a.V = vocab;
+  a.l1 = l1_out;
+  a.ce = ce_out;
+  a.stats = stats;
+  a.flags = status_flags;
+  a.amax = argmax_out;
+  a.g_ce = grad_ce;
+  a.g_l1 = grad_l1;
+  a.dx = static_cast<uint16_t*>(grad_logits);
   return launch_fwd(a, static_cast<hipStream_t>(stream));
 }
 

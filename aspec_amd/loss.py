@@ -136,22 +136,87 @@ def ce_l1_from_logits(logits, targets, teacher=None, *, teacher_indices=None, ig
         raise ValueError("targets must be one int64 class index per logit row on the logits device")
     targets = targets.reshape(-1).contiguous()
     if teacher is not None:
-        if teacher.requires_grad:
-            raise ValueError("tiled L1 requires frozen teacher logits")
-        if teacher.dtype != logits.dtype or not teacher.is_contiguous() or teacher.device != logits.device:
-            raise ValueError("draft and teacher logits must share shape and dtype")
-        if teacher_indices is None and teacher.shape != logits.shape:
-            raise ValueError("draft and teacher logits must share shape and dtype")
-        if teacher_indices is not None and (
-                teacher.ndim != 2 or teacher.shape[-1] != logits.shape[-1] or teacher.shape[0] == 0
-                or teacher_indices.dtype != torch.int64 or teacher_indices.numel() != rows
-                or teacher_indices.device != logits.device):
-            raise ValueError("indexed teacher requires a nonempty 2D table and one contiguous CUDA "
-                             "int64 index per Draft row")
+        _check_teacher(logits, teacher, teacher_indices, rows)
         if teacher_indices is not None:
             teacher_indices = teacher_indices.reshape(-1).contiguous()
     return _CeL1.apply(logits, targets, teacher, teacher_indices, ignore_index, return_argmax,
                        _replay_cache)
+
+
+def _check_teacher(logits, teacher, teacher_indices, rows):
+    if teacher.requires_grad:
+        raise ValueError("tiled L1 requires frozen teacher logits")
+    if teacher.dtype != logits.dtype or not teacher.is_contiguous() or teacher.device != logits.device:
+        raise ValueError("draft and teacher logits must share shape and dtype")
+    if teacher_indices is None and teacher.shape != logits.shape:
+        raise ValueError("draft and teacher logits must share shape and dtype")
+    if teacher_indices is not None and (
+            teacher.ndim != 2 or teacher.shape[-1] != logits.shape[-1] or teacher.shape[0] == 0
+            or teacher_indices.dtype != torch.int64 or teacher_indices.numel() != rows
+            or teacher_indices.device != logits.device):
+        raise ValueError("indexed teacher requires a nonempty 2D table and one contiguous CUDA "
+                         "int64 index per Draft row")
+
+
+def fused_grad_vocab(vocab: int) -> bool:
+    """Whether `ce_l1_fused_grad` covers this vocabulary size (V % 8 == 0, V <= 32768)."""
+    return vocab % 8 == 0 and vocab <= 32768
+
+
+def fused_grad_supported(logits) -> bool:
+    """Whether `ce_l1_fused_grad` runs as one kernel for these logits (a covered vocabulary and
+    16-byte aligned rows)."""
+    return fused_grad_vocab(logits.shape[-1]) and logits.data_ptr() % 16 == 0
+
+
+def ce_l1_fused_grad(logits, targets, teacher, *, ce_weights, l1_weights, teacher_indices=None,
+                     ignore_index=-100, return_argmax=False, in_place=False):
+    """Per-row (ce, l1[, argmax]) and dlogits of sum_r (ce_weights[r] ce[r] + l1_weights[r] l1[r])
+    from one pass over the logits (no autograd). The DSpark loss numerator
+    ce_alpha * ce_num + l1_alpha * l1_num (dspark.py:485-491) has this form with the weights
+    alpha * eval mask * decay, so its backward needs no second read of the logits and teacher.
+    With `in_place` the dlogits overwrite `logits` (which the caller must no longer need).
+    Out-of-range teacher indices / targets raise ValueError. Returns (ce, l1, dlogits[, argmax]);
+    raises NotImplementedError where `fused_grad_supported` is False."""
+    ce, l1, dlogits, amax, check = _ce_l1_fused(logits, targets, teacher, ce_weights, l1_weights,
+                                                teacher_indices, ignore_index, return_argmax, in_place)
+    check.raise_if_bad()
+    if return_argmax:
+        return ce, l1, dlogits, amax
+    return ce, l1, dlogits
+
+
+def _ce_l1_fused(logits, targets, teacher, ce_weights, l1_weights, teacher_indices, ignore_index,
+                 return_argmax, in_place):
+    """The launch behind `ce_l1_fused_grad`; returns (ce, l1, dlogits, argmax, IndexCheck) with the
+    index check still to be read."""
+    _check_logits(logits)
+    vocab = logits.shape[-1]
+    rows = logits.numel() // vocab
+    if targets.dtype != torch.int64 or targets.numel() != rows or targets.device != logits.device:
+        raise ValueError("targets must be one int64 class index per logit row on the logits device")
+    _check_teacher(logits, teacher, teacher_indices, rows)
+    for w in (ce_weights, l1_weights):
+        if w.numel() != rows or w.device != logits.device:
+            raise ValueError("objective weights must hold one value per logit row on the logits device")
+    targets = targets.reshape(-1).contiguous()
+    indices = None if teacher_indices is None else teacher_indices.reshape(-1).contiguous()
+    gce = ce_weights.reshape(-1).to(torch.float32).contiguous()
+    gl1 = l1_weights.reshape(-1).to(torch.float32).contiguous()
+    dev = logits.device
+    trows = teacher.shape[0] if indices is not None else rows
+    stats = torch.empty((rows, STATS), dtype=torch.float32, device=dev)
+    ce = torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev)
+    l1 = torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev)
+    amax = torch.empty(logits.shape[:-1], dtype=torch.int64, device=dev) if return_argmax else None
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    dlogits = logits if in_place else torch.empty_like(logits)
+    with _timing.region("loss_fused"):
+        _lib.call("aspec_ce_l1_fused_fwd_bwd", _lib.ptr(logits), _lib.ptr(teacher), _lib.ptr(indices),
+                  trows, _lib.ptr(targets), ignore_index, rows, vocab, _lib.ptr(gce), _lib.ptr(gl1),
+                  _lib.ptr(l1), _lib.ptr(ce), _lib.ptr(amax), _lib.ptr(stats), _lib.ptr(dlogits),
+                  _lib.ptr(flags), _lib.stream_handle(dev))
+    return ce, l1, dlogits, amax, IndexCheck(flags)
 
 
 def cross_entropy(logits, targets, ignore_index=-100):

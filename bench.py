@@ -7,9 +7,10 @@ One step = one packed 4096-token row through the draft hot path, inputs resident
      the frozen-teacher table = target_hidden[4096, 4096] @ W^T (no grad); library GEMMs
      (hipBLASLt / rocBLAS) with the solutions recorded in aspec_amd/tuning/head_gemms_gfx950.csv,
   4. fused CE + softmax-L1 (HIP, indexed teacher rows), objective (0.1 CE + 0.9 L1) weighted by the
-     DSpark eval mask x exp(-k/4) decay, normalised by the weight sum,
-  5. backward: dlogits (HIP), dO = dlogits @ W (on the frozen head's transposed copy), attention
-     backward (HIP);
+     DSpark eval mask x exp(-k/4) decay, normalised by the weight sum; the same pass writes the
+     objective's dlogits over the logits (aspec_amd.head_loss; --unfused-head runs the loss
+     forward and backward kernels instead),
+  5. backward: dO = dlogits @ W (on the frozen head's transposed copy), attention backward (HIP);
   before the head: injected-anchor validation, output-block counts and the DSpark targets (labels,
   eval mask, decay weights) from the anchors (HIP).
 The teacher table runs on a second stream while the host performs the step's host-side checks
@@ -67,6 +68,9 @@ def parse():
     p.add_argument("--no-kernel-timing", action="store_true", help="no per-kernel HIP events")
     p.add_argument("--no-attention-configs", action="store_true",
                    help="skip the attention-only timings at configs 3 and 4")
+    p.add_argument("--unfused-head", action="store_true",
+                   help="head as separate GEMM, loss forward and loss backward kernels (the fused "
+                        "operator writes dlogits in the loss forward)")
     p.add_argument("--serial", action="store_true",
                    help="timed steps without the stream overlaps (each kernel alone on the GPU, as "
                         "for the rocprofv3 kernel traces and counters)")
@@ -153,13 +157,14 @@ class _Head:
         return HeadProjection
 
 
-def step(x, head_fn, overlap=True):
+def step(x, head_fn, overlap=True, fused_head=True):
     import torch
 
     from aspec_amd import _timing
     from aspec_amd.anchors import validate_injected_anchors
     from aspec_amd.direct_cp import DirectCPMetadata, direct_cp_attention_from_kv
     from aspec_amd.targets import dspark_targets
+    from aspec_amd.head_loss import selective_head_objective
     from aspec_amd.loss import ce_l1_from_logits
     from aspec_amd.output_blocks import output_block_counts
 
@@ -194,13 +199,23 @@ def step(x, head_fn, overlap=True):
         x[name].grad = None
     out, _ = direct_cp_attention_from_kv(x["q"], x["k"], x["v"], meta)
     hidden = out.transpose(1, 2).reshape(w.num_queries, w.q_heads * w.head_dim)
-    logits = head_fn.apply(hidden, x["head"], x["head_t"])
-    main.wait_event(teacher_done)
-    ce, l1 = ce_l1_from_logits(logits, targets.target_ids.reshape(-1), teacher,
-                               teacher_indices=targets.teacher_index.reshape(-1))
     wts = targets.weights.reshape(-1)
-    # (0.1 sum(w ce) + 0.9 sum(w l1)) / sum(w), as one add and one dot product (fewer launches)
-    loss = torch.dot(torch.add(l1, ce, alpha=CE_ALPHA / L1_ALPHA), wts) * (L1_ALPHA / wts.sum().clamp(min=1e-6))
+    if fused_head:
+        # the objective (0.1 sum(w ce) + 0.9 sum(w l1)) / sum(w) as one operator: vocab GEMM, then
+        # one loss pass that also writes dlogits (aspec_amd.head_loss)
+        scale = 1.0 / wts.sum().clamp(min=1e-6)
+        loss, _, _ = selective_head_objective(
+            hidden, x["head"], targets.target_ids.reshape(-1), teacher,
+            teacher_indices=targets.teacher_index.reshape(-1), weight_t=x["head_t"],
+            ce_weights=wts * (CE_ALPHA * scale), l1_weights=wts * (L1_ALPHA * scale),
+            teacher_ready=teacher_done)
+    else:
+        logits = head_fn.apply(hidden, x["head"], x["head_t"])
+        main.wait_event(teacher_done)
+        ce, l1 = ce_l1_from_logits(logits, targets.target_ids.reshape(-1), teacher,
+                                   teacher_indices=targets.teacher_index.reshape(-1))
+        # (0.1 sum(w ce) + 0.9 sum(w l1)) / sum(w), as one add and one dot product (fewer launches)
+        loss = torch.dot(torch.add(l1, ce, alpha=CE_ALPHA / L1_ALPHA), wts) * (L1_ALPHA / wts.sum().clamp(min=1e-6))
     loss.backward()
     return loss
 
@@ -318,6 +333,8 @@ def kernel_work(w, device, teacher_rows):
         "teacher_gemm": ("mfma", 2 * ctx * VOCAB * HIDDEN),
         "loss_fwd": ("hbm", (rows + teacher_rows) * VOCAB * 2),
         "loss_bwd": ("hbm", (2 * rows + teacher_rows) * VOCAB * 2),
+        # fused forward + dlogits: each draft row and distinct teacher row read once, dx written
+        "loss_fused": ("hbm", (2 * rows + teacher_rows) * VOCAB * 2),
         "thd_row_metadata": ("hbm", w.num_blocks * 17 + ctx * 16 + rows * 4 * 4 + w.num_keys * 4 * 4 + rows * 5 * 4),
         "attn_plan_build": ("hbm", rows * 5 * 4 * 2),
         # anchors + keep in, masked anchors out, two loss-mask and two doc reads per kept anchor
@@ -333,6 +350,7 @@ def kernel_work(w, device, teacher_rows):
 _REGION_KERNEL = {"attn_fwd": "attn_fwd_kernel<4>", "attn_bwd_dq": "attn_bwd_dq_kernel<4>",
                   "attn_bwd_dkdv": "attn_bwd_dkdv_kernel<4>", "attn_bwd_prepare": "attn_bwd_pre_kernel",
                   "loss_fwd": "loss_fwd_persistent<8, false, true>", "loss_bwd": "loss_bwd_rows_kernel",
+                  "loss_fused": "loss_fwd_persistent<8, false, true, true>",
                   "head_gemm_fwd": "Custom_Cijk_Alik_Bljk_BBS_BH_MT256x256x64_MI16x16x1_UserArgs_shortname0_gfx950",
                   "qk_norm_rope_fwd": "qk_norm_rope_fwd_kernel", "qk_norm_rope_bwd": "qk_norm_rope_bwd_kernel"}
 _LIBRARY_REGIONS = ("head_gemm_fwd", "head_gemm_dgrad", "teacher_gemm")
@@ -720,13 +738,14 @@ def main():
     from aspec_amd.direct_cp import set_backward_overlap
 
     overlap = not args.serial
+    fused = not args.unfused_head
     set_backward_overlap(overlap)
     for _ in range(args.warmup):
-        step(x, head_fn, overlap)
+        step(x, head_fn, overlap, fused)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        loss = step(x, head_fn, overlap)
+        loss = step(x, head_fn, overlap, fused)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     if not torch.isfinite(loss):
@@ -736,12 +755,12 @@ def main():
         # Per-kernel durations with every kernel alone on the GPU: the same steps again with the
         # two overlaps (teacher table, dQ beside dK/dV) off.
         set_backward_overlap(False)
-        step(x, head_fn, False)
+        step(x, head_fn, False, fused)
         torch.cuda.synchronize()
         _timing.reset()
         _timing.enable(True)
         for _ in range(args.steps):
-            step(x, head_fn, False)
+            step(x, head_fn, False, fused)
         torch.cuda.synchronize()
         _timing.enable(False)
         kernels = _timing.summary()
@@ -750,7 +769,8 @@ def main():
     teacher_rows = unique_teacher_rows(x)
     pairs, work = kernel_work(w, device, teacher_rows)
     # the loss bytes as the per-row accounting states them (every row reads a full teacher row)
-    survey_bytes = {"loss_fwd": 2 * w.num_queries * VOCAB * 2, "loss_bwd": 3 * w.num_queries * VOCAB * 2}
+    survey_bytes = {"loss_fwd": 2 * w.num_queries * VOCAB * 2, "loss_bwd": 3 * w.num_queries * VOCAB * 2,
+                    "loss_fused": 3 * w.num_queries * VOCAB * 2}
     per_kernel = {}
     for name, stats in kernels.items():
         bound, amount = work.get(name, (None, None))
@@ -823,6 +843,8 @@ def main():
             "parallelism": "single GPU, CP=1",
             "streams": ("one (--serial)" if args.serial else
                         "two: teacher table and attention dQ on a second stream"),
+            "head_loss": ("one pass: CE + L1 + dlogits (selective_head_objective)" if fused
+                          else "loss forward and backward kernels"),
             "head_gemms": (f"library GEMMs, TunableOp solutions from {gemm_solutions}" if gemm_solutions
                            else "library GEMMs, default solutions"),
         },

@@ -268,6 +268,24 @@ int aspec_ce_l1_bwd(const void* logits, const void* teacher, const int64_t* teac
                     int64_t vocab, const float* stats, const float* grad_l1, const float* grad_ce,
                     void* grad_logits, void* stream);
 
+/*
+ * aspec_ce_l1_argmax_fwd and aspec_ce_l1_bwd in one pass, for an objective whose per-row weights
+ * are known before the forward: sum_r (grad_ce[r] * ce[r] + grad_l1[r] * l1[r]) (the DSpark loss
+ * numerator ce_alpha * ce_num + l1_alpha * l1_num, aspec/models/dspark.py:485-491, with the
+ * eval-mask x decay weights folded into grad_ce / grad_l1). Writes l1_out, ce_out, argmax_out (may
+ * be NULL), stats, and grad_logits = the aspec_ce_l1_bwd result for these gradients, each row once
+ * its statistics are final. grad_logits may be the logits buffer itself (in place). Needs a teacher,
+ * vocab % 8 == 0, vocab <= 32768 and 16-byte aligned rows (status 2 otherwise). Removes the
+ * backward's second read of the logits and teacher rows: the selective head's vocab GEMM + CE/L1
+ * (aspec/models/dspark.py:553-612, aspec/models/ops/tiled_l1.py:31-127) then moves its logits
+ * through HBM once.
+ */
+int aspec_ce_l1_fused_fwd_bwd(const void* logits, const void* teacher, const int64_t* teacher_index,
+                              int64_t teacher_rows, const int64_t* targets, int64_t ignore_index,
+                              int64_t rows, int64_t vocab, const float* grad_ce, const float* grad_l1,
+                              float* l1_out, float* ce_out, int64_t* argmax_out, float* stats,
+                              void* grad_logits, int32_t* status_flags, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Row-level operations around the attention and loss: packing, anchors, output blocks, targets.
  * ------------------------------------------------------------------------------------------- */
