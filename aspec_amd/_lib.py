@@ -69,6 +69,7 @@ SIGNATURES = {
     "aspec_ce_l1_fused_fwd_bwd": (
         _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64] + [_c_void_p] * 9
     ),
+    "aspec_scale_bf16_by_device_scalar": (_int, [_c_void_p, _i64, _c_void_p, _c_void_p]),
     "aspec_pack_copy": (_int, [_c_void_p, _i64, _c_void_p]),
     "aspec_pack_row_metadata": (_int, [_c_void_p, _i64, _i64] + [_c_void_p] * 4),
     "aspec_sample_document_anchors": (
@@ -113,7 +114,7 @@ SIGNATURES = {
     "aspec_pack_work_aware_rows": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lock = threading.Lock()
 _lib = None

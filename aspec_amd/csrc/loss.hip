@@ -775,6 +775,33 @@ int launch_bwd(const LossArgs& a, hipStream_t s) {
   return check_launch("loss backward");
 }
 
+// Two bf16 in one word, each times s: fp32 product, one round to nearest even.
+__device__ __forceinline__ uint32_t scale_bf16_pair(uint32_t w, float s) {
+  return pack_bf16x2(__uint_as_float(w << 16) * s, __uint_as_float(w & 0xffff0000u) * s);
+}
+
+// x *= s in place over n bf16 values, s read on the device. When s == 1 every product equals its
+// input bit for bit, so each workgroup returns before touching x (the usual upstream gradient of a
+// loss: the multiply costs a launch instead of a pass over x). n8 16-byte groups, then the tail.
+__global__ void __launch_bounds__(256) scale_bf16_kernel(uint16_t* x, int64_t n, int64_t n8,
+                                                         const float* scalar) {
+  const float s = scalar_read(scalar);
+  if (s == 1.0f) return;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  uint4* v = reinterpret_cast<uint4*>(x);
+  for (int64_t i = first; i < n8; i += stride) {
+    uint4 w = v[i];
+    w.x = scale_bf16_pair(w.x, s);
+    w.y = scale_bf16_pair(w.y, s);
+    w.z = scale_bf16_pair(w.z, s);
+    w.w = scale_bf16_pair(w.w, s);
+    v[i] = w;
+  }
+  for (int64_t i = n8 * 8 + first; i < n; i += stride)
+    x[i] = f32_to_bf16_bits(bf16_to_f32(x[i]) * s);
+}
+
 int check_common(int64_t rows, int64_t V, const void* x) {
   if (rows <= 0 || V <= 0 || !x)
     return set_error(ASPEC_ERR_INVALID, "loss kernels require nonempty logits with a vocabulary dimension");
@@ -851,6 +878,19 @@ extern "C" int aspec_ce_l1_fused_fwd_bwd(const void* logits, const void* teacher
   a.g_l1 = grad_l1;
   a.dx = static_cast<uint16_t*>(grad_logits);
   return launch_fwd(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int aspec_scale_bf16_by_device_scalar(void* x, int64_t n, const float* scalar,
+                                                  void* stream) {
+  if (n < 0 || (n > 0 && (!x || !scalar)))
+    return set_error(ASPEC_ERR_INVALID, "scaling needs a buffer, a size >= 0 and a device scalar");
+  if (n == 0) return ASPEC_OK;
+  const int64_t n8 = (reinterpret_cast<uintptr_t>(x) & 15) == 0 ? n / 8 : 0;
+  const int64_t work = std::max<int64_t>(n8, n - n8 * 8);
+  const int64_t grid = std::min<int64_t>((work + 255) / 256, 1024);
+  hipLaunchKernelGGL(scale_bf16_kernel, dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<uint16_t*>(x), n, n8, scalar);
+  return check_launch("bf16 scale");
 }
 
 extern "C" int aspec_ce_l1_fwd(const void* logits, const void* teacher, const int64_t* teacher_index,

@@ -6,7 +6,8 @@ teacher, and the model combines them into `ce_alpha * ce_num + l1_alpha * l1_num
 (dspark.py:485-491) with per-row eval-mask x decay weights. With those weights known before the
 forward, `selective_head_objective` computes logits = hidden W^T with the library GEMM, then one
 loss pass (`aspec_ce_l1_fused_fwd_bwd`) writes CE, L1 and the objective's dlogits over the logits
-in place; the backward is dh = g * dlogits W. Against the unfused composition (GEMM, loss forward,
+in place; the backward is dh = g * dlogits W (g scales dh in place on the device, a no-op pass when
+g == 1). Against the unfused composition (GEMM, loss forward,
 loss backward, dgrad GEMM) this drops the backward's second read of the logits and teacher rows and
 one kernel launch. Vocabularies the fused pass does not cover (V % 8 != 0 or V > 32768) run that
 composition instead, with the same results.
@@ -17,7 +18,7 @@ from __future__ import annotations
 import torch
 from torch.autograd.function import once_differentiable
 
-from aspec_amd import _timing
+from aspec_amd import _lib, _timing
 from aspec_amd.loss import _ce_l1_fused, ce_l1_from_logits, fused_grad_vocab
 
 
@@ -54,7 +55,10 @@ class _SelectiveHeadObjective(torch.autograd.Function):
         with _timing.region("head_gemm_dgrad"):
             dh = torch.matmul(dlogits, weight_t.t())
         if grad_objective is not None:
-            dh.mul_(grad_objective.to(dh.dtype))
+            # dh *= g on the device; g is exactly 1 for loss.backward(), and then nothing is written
+            g = grad_objective.detach().reshape(()).to(device=dh.device, dtype=torch.float32)
+            _lib.call("aspec_scale_bf16_by_device_scalar", dh.data_ptr(), dh.numel(), g.data_ptr(),
+                      _lib.stream_handle(dh.device))
         return dh, None, None, None, None, None, None, None, None, None, None
 
 

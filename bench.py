@@ -618,13 +618,14 @@ def parity_block(x, seed):
     """Errors of the HIP path against the oracle on the bench's own config-2 inputs (outside the
     timed region): attention O / LSE / dQ / dK / dV of every KV group against the chunked fp32
     oracle (oracle/attention.py), with a seeded dO and LSE gradient; and CE / L1 / dlogits of the
-    fused loss on 512 sampled rows of the bench's own logits (head GEMM of the attention output,
-    indexed teacher table) against the fp64 oracle (oracle/loss.py). Tolerances are the
+    step's one-pass loss (`ce_l1_fused_grad`, the step's objective weights) on 512 sampled rows of
+    the bench's own logits (head GEMM of the attention output, indexed teacher table) against the
+    fp64 oracle (oracle/loss.py). Tolerances are the
     reference's (tests/test_thd_attention.py:218-225, tests/test_tiled_l1.py:28-46)."""
     import torch
 
     from aspec_amd.direct_cp import DirectCPMetadata, direct_cp_attention_from_kv
-    from aspec_amd.loss import ce_l1_from_logits
+    from aspec_amd.loss import ce_l1_fused_grad
     from aspec_amd.targets import dspark_targets
     from oracle import attention as A
     from oracle import loss as L
@@ -682,10 +683,9 @@ def parity_block(x, seed):
                              loss_decay_gamma=DECAY_GAMMA, ctx_doc_ids=docs)
     tid, tix = targets.target_ids.reshape(-1), targets.teacher_index.reshape(-1)
     wts = targets.weights.reshape(-1)
-    xin = logits.clone().requires_grad_()
-    ce, l1 = ce_l1_from_logits(xin, tid, teacher, teacher_indices=tix)
     gce, gl1 = CE_ALPHA * wts / wts.sum(), L1_ALPHA * wts / wts.sum()
-    ((ce * gce).sum() + (l1 * gl1).sum()).backward()
+    ce, l1, dlogits = ce_l1_fused_grad(logits, tid, teacher, ce_weights=gce, l1_weights=gl1,
+                                       teacher_indices=tix)
     torch.cuda.synchronize()
     rows = np.random.default_rng(seed).choice(w.num_queries, 512, replace=False)
     ri = torch.as_tensor(rows, device=device)
@@ -696,9 +696,9 @@ def parity_block(x, seed):
     ref_g = (L.cross_entropy_grad(xd, td, gce[ri].double().cpu().numpy())
              + L.l1_grad(xd, yd, gl1[ri].double().cpu().numpy()))
     loss_pairs = {
-        "CE": ([(ce.detach()[ri].cpu(), torch.as_tensor(ref_ce))], 2e-5, 2e-6),
-        "L1": ([(l1.detach()[ri].cpu(), torch.as_tensor(ref_l1))], 2e-6, 2e-6),
-        "dlogits": ([(xin.grad[ri].cpu(), torch.as_tensor(ref_g).to(torch.bfloat16))], 1e-6, 0.02),
+        "CE": ([(ce[ri].cpu(), torch.as_tensor(ref_ce))], 2e-5, 2e-6),
+        "L1": ([(l1[ri].cpu(), torch.as_tensor(ref_l1))], 2e-6, 2e-6),
+        "dlogits": ([(dlogits[ri].cpu(), torch.as_tensor(ref_g).to(torch.bfloat16))], 1e-6, 0.02),
     }
     for name, (pr, atol, rtol) in loss_pairs.items():
         max_abs, rel = _errors(pr)

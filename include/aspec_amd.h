@@ -286,6 +286,14 @@ int aspec_ce_l1_fused_fwd_bwd(const void* logits, const void* teacher, const int
                               float* l1_out, float* ce_out, int64_t* argmax_out, float* stats,
                               void* grad_logits, int32_t* status_flags, void* stream);
 
+/*
+ * x *= *scalar in place over n bf16 values (fp32 product, one round to nearest even), the scalar
+ * read on the device. The upstream gradient of the fused objective scales the dgrad GEMM's dh
+ * with it (the gradient a loss's backward receives, aspec/models/dspark.py:485-491). A scalar of
+ * exactly 1 leaves x untouched (every product would equal its input), without a host read.
+ */
+int aspec_scale_bf16_by_device_scalar(void* x, int64_t n, const float* scalar, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Row-level operations around the attention and loss: packing, anchors, output blocks, targets.
  * ------------------------------------------------------------------------------------------- */

@@ -10,6 +10,8 @@ selective-head objective operator built on it.
 * identical draft and teacher rows: the L1 part of dlogits is exactly zero (the CE-only result);
 * in place equals out of place bitwise; out-of-range indices raise; uncovered vocabularies raise
   NotImplementedError;
+* the device-scalar scale of dh (`aspec_scale_bf16_by_device_scalar`) equals torch's fp32 product
+  rounded once, on aligned, unaligned and tail elements, and leaves the buffer untouched for 1;
 * `selective_head_objective` (GEMM + fused pass, dh = g dlogits W) against the unfused composition
   of the same library GEMM, `ce_l1_from_logits` and autograd (CE, L1 bitwise, the objective), and
   both against dh in fp64, also on the fallback vocabulary.
@@ -160,3 +162,40 @@ def test_selective_head_objective_equals_unfused_composition(gpu, vocab):
     err_f, err_u = _rel(hf.grad.cpu(), ref), _rel(hu.grad.cpu(), ref)
     print(f"objective V={vocab}: dh rel_l2 vs fp64 fused {err_f:.2e} unfused {err_u:.2e}")
     assert err_f < 1e-2 and err_f < 1.6 * err_u + 1e-4
+
+
+@pytest.mark.parametrize("offset,n", [(0, 8 * 1000), (0, 8 * 1000 + 5), (3, 777), (1, 3)])
+def test_device_scalar_scale(gpu, offset, n):
+    from aspec_amd import _lib
+
+    base = torch.randn(n + offset, device=gpu).to(torch.bfloat16)
+    base[offset::97] = torch.inf
+    x = base[offset:]
+    before = x.clone()
+    for value in (0.37, -3.0, 1.0):
+        s = torch.tensor(value, device=gpu)
+        y = base.clone()[offset:]  # the same alignment as x
+        _lib.call("aspec_scale_bf16_by_device_scalar", y.data_ptr(), n, s.data_ptr(),
+                  _lib.stream_handle(gpu))
+        expect = (x.float() * value).to(torch.bfloat16)  # fp32 product, one round to nearest even
+        assert torch.equal(y.view(torch.int16), expect.view(torch.int16)), value
+    z = torch.full((1,), float("nan"), device=gpu, dtype=torch.bfloat16)
+    _lib.call("aspec_scale_bf16_by_device_scalar", z.data_ptr(), 1, torch.tensor(1.0, device=gpu).data_ptr(),
+              _lib.stream_handle(gpu))
+    assert torch.isnan(z).all() and torch.equal(x, before)
+
+
+def test_objective_unit_upstream_gradient_is_dlogits_times_w(gpu):
+    g = torch.Generator(device=gpu).manual_seed(3)
+    rows, hid, vocab = 256, 128, 4096
+    h = (torch.randn(rows, hid, device=gpu, generator=g) * 0.5).to(torch.bfloat16).requires_grad_()
+    w = (torch.randn(vocab, hid, device=gpu, generator=g) * 0.05).to(torch.bfloat16)
+    teacher = (torch.randn(rows, vocab, device=gpu, generator=g)).to(torch.bfloat16)
+    t = torch.randint(0, vocab, (rows,), device=gpu, generator=g)
+    w_ce = torch.rand(rows, device=gpu, generator=g)
+    w_l1 = torch.rand(rows, device=gpu, generator=g)
+    obj, _, _ = selective_head_objective(h, w, t, teacher, ce_weights=w_ce, l1_weights=w_l1)
+    obj.backward()
+    logits = torch.matmul(h.detach(), w.t())
+    _, _, dlogits = ce_l1_fused_grad(logits, t, teacher, ce_weights=w_ce, l1_weights=w_l1)
+    assert torch.equal(h.grad, torch.matmul(dlogits, w.t().contiguous().t()))
