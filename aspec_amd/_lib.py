@@ -17,6 +17,7 @@ _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
 _f32 = ctypes.c_float
+_f64 = ctypes.c_double
 _size_p = ctypes.POINTER(ctypes.c_size_t)
 
 # name -> (restype, argtypes); the exact export list of include/aspec_amd.h.
@@ -70,6 +71,15 @@ SIGNATURES = {
         _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64] + [_c_void_p] * 9
     ),
     "aspec_scale_bf16_by_device_scalar": (_int, [_c_void_p, _i64, _c_void_p, _c_void_p]),
+    "aspec_sampling_stats_floats": (_int, []),
+    "aspec_sampling_logits_fwd": (_int, [_c_void_p, _i64, _i64, _f64, _f64, _i64] + [_c_void_p] * 3),
+    "aspec_sampling_logits_bwd": (_int, [_c_void_p] * 3 + [_i64, _i64] + [_c_void_p] * 2),
+    "aspec_sampled_l1_stats_floats": (_int, []),
+    "aspec_sampled_l1_fwd": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _f64, _f64, _i64, _f64, _f64, _i64]
+        + [_c_void_p] * 4
+    ),
+    "aspec_sampled_l1_bwd": (_int, [_c_void_p] * 3 + [_i64, _i64, _i64] + [_c_void_p] * 4),
     "aspec_pack_copy": (_int, [_c_void_p, _i64, _c_void_p]),
     "aspec_pack_row_metadata": (_int, [_c_void_p, _i64, _i64] + [_c_void_p] * 4),
     "aspec_sample_document_anchors": (
@@ -114,7 +124,7 @@ SIGNATURES = {
     "aspec_pack_work_aware_rows": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _lock = threading.Lock()
 _lib = None

@@ -35,9 +35,9 @@ COMMON_FLAGS = [
     # the wrong register class fails the build instead of being encoded silently.
     "-mllvm", "-verify-machineinstrs",
 ]
-# The loss kernels must evaluate draft and teacher probabilities with identical instruction
-# sequences; contraction into FMAs stays off there.
-PER_FILE_FLAGS = {"loss.hip": ["-ffp-contract=off"]}
+# The loss and sampled-L1 kernels must evaluate draft and teacher probabilities (and the
+# forward's and backward's) with identical instruction sequences; contraction into FMAs stays off.
+PER_FILE_FLAGS = {"loss.hip": ["-ffp-contract=off"], "sampling.hip": ["-ffp-contract=off"]}
 
 
 def hipcc() -> str:

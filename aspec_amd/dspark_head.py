@@ -25,6 +25,7 @@ from torch.autograd.function import once_differentiable
 
 from . import _timing
 from .loss import ce_l1_from_logits
+from .sampling import DEFAULT_SAMPLING, compiled_l1_from_logits
 
 __all__ = [
     "VanillaMarkov",
@@ -190,7 +191,7 @@ def dspark_prediction_terms(hidden, target_ids, prev_ids, head_weight, aligned_t
                             confidence_head_with_markov=True, l1_loss_alpha=1.0,
                             confidence_head_alpha=0.0, prediction_start=0, block_size=None,
                             cached_target_logits=None, cached_draft_logits=None,
-                            cached_target_positions=None, loss_cache=None):
+                            cached_target_positions=None, loss_cache=None, l1_sampling=None):
     """Additive DSpark head terms for one block slice (aspec/models/dspark.py:553-636):
     (ce_num, l1_num, conf_num, position_loss, position_correct, acceptance_totals).
 
@@ -203,6 +204,11 @@ def dspark_prediction_terms(hidden, target_ids, prev_ids, head_weight, aligned_t
         head_weight (no Markov bias).
     `loss_cache` is the head chunk's checkpoint-replay dict (dspark.py:473, 602): filled by the
     first forward, replayed without a loss forward kernel on the checkpoint recompute.
+    `l1_sampling` = (target_sampling, draft_sampling), each (temperature, top_p, top_k), filters
+    both distributions before the L1 (`DSparkModel(l1_target_sampling=..., l1_draft_sampling=...)`,
+    dspark.py:111-112, 606-609): CE and the argmax still come from the raw logits, the L1 from
+    `aspec_amd.sampling.compiled_l1_from_logits`; as in the reference, `loss_cache` then serves
+    neither term.
     """
     if cached_draft_logits is not None:
         logits = cached_draft_logits
@@ -231,9 +237,17 @@ def dspark_prediction_terms(hidden, target_ids, prev_ids, head_weight, aligned_t
             ).view_as(logits)
             teacher = teacher.detach().contiguous().reshape(-1, vocab)
     flat = logits.reshape(-1, vocab).contiguous()
-    ce, l1, argmax = ce_l1_from_logits(
-        flat, target_ids.reshape(-1).long().contiguous(), teacher, teacher_indices=teacher_index,
-        return_argmax=True, _replay_cache=loss_cache)
+    sampled = l1_sampling is not None and tuple(map(tuple, l1_sampling)) != (DEFAULT_SAMPLING,
+                                                                              DEFAULT_SAMPLING)
+    if sampled and teacher is not None:
+        ce, _, argmax = ce_l1_from_logits(flat, target_ids.reshape(-1).long().contiguous(), None,
+                                          return_argmax=True)
+        l1 = compiled_l1_from_logits(flat, teacher, l1_sampling[0], l1_sampling[1],
+                                     teacher_indices=teacher_index)
+    else:
+        ce, l1, argmax = ce_l1_from_logits(
+            flat, target_ids.reshape(-1).long().contiguous(), teacher, teacher_indices=teacher_index,
+            return_argmax=True, _replay_cache=loss_cache)
     ce = ce.view_as(weights)
     ce_num = (ce * weights).sum()
     l1_num = logits.new_zeros((), dtype=torch.float32)

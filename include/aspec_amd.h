@@ -294,6 +294,45 @@ int aspec_ce_l1_fused_fwd_bwd(const void* logits, const void* teacher, const int
  */
 int aspec_scale_bf16_by_device_scalar(void* x, int64_t n, const float* scalar, void* stream);
 
+/*
+ * Sampled L1 (aspec/models/ops/loss.py:57-89; DSparkModel._prediction_terms with l1 sampling,
+ * aspec/models/dspark.py:606-609). Per row and side the logits are filtered as
+ * sampling_logits(x, (temperature, top_p, top_k)): scaled = (x - max x) * (1/T) when T != 1
+ * (else x), ordered descending with ties by token index; a token is kept iff its rank < top_k
+ * (0 < top_k < V) and the softmax(scaled) mass of the tokens before it <= top_p (top_p < 1).
+ * Parameters: temperature finite > 0, top_p in (0, 1], top_k -1 or >= 1 (status 1 otherwise).
+ * bf16 logits, any V up to 2^24, rows < 2^31. No sort: a binary search over the 16-bit bf16
+ * keys per row (the row in registers up to 98304 tokens).
+ *
+ * aspec_sampling_logits_fwd writes the filtered fp32 logits ([rows][vocab], -inf outside the
+ * support) and aspec_sampling_stats_floats() floats of stats per row; aspec_sampling_logits_bwd
+ * maps an fp32 gradient of them to the bf16 logits (keep * g / T, with the max subtraction's
+ * gradient shared by the tokens equal to the max).
+ */
+int aspec_sampling_stats_floats(void);
+int aspec_sampling_logits_fwd(const void* logits, int64_t rows, int64_t vocab, double temperature,
+                              double top_p, int64_t top_k, float* out, float* stats, void* stream);
+int aspec_sampling_logits_bwd(const void* logits, const float* grad_out, const float* stats,
+                              int64_t rows, int64_t vocab, void* grad_logits, void* stream);
+
+/*
+ * l1_out[r] = sum |softmax_kept(draft) - softmax_kept(teacher)| with draft_* and target_* the two
+ * sides' filters (compiled_l1_from_logits(logits, target, target_sampling, draft_sampling),
+ * aspec/models/ops/loss.py:83-89); the teacher row is teacher_index[r] when given (an
+ * out-of-range index sets bit 0 of status_flags and gives a NaN row). Stats:
+ * aspec_sampled_l1_stats_floats() floats per row. The backward writes the bf16 draft gradient
+ * grad_l1[r] / T * p * (sign(p - q) - sum p sign(p - q)); the teacher is frozen.
+ */
+int aspec_sampled_l1_stats_floats(void);
+int aspec_sampled_l1_fwd(const void* logits, const void* teacher, const int64_t* teacher_index,
+                         int64_t teacher_rows, int64_t rows, int64_t vocab, double draft_temperature,
+                         double draft_top_p, int64_t draft_top_k, double target_temperature,
+                         double target_top_p, int64_t target_top_k, float* l1_out, float* stats,
+                         int32_t* status_flags, void* stream);
+int aspec_sampled_l1_bwd(const void* logits, const void* teacher, const int64_t* teacher_index,
+                         int64_t teacher_rows, int64_t rows, int64_t vocab, const float* stats,
+                         const float* grad_l1, void* grad_logits, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Row-level operations around the attention and loss: packing, anchors, output blocks, targets.
  * ------------------------------------------------------------------------------------------- */
