@@ -94,16 +94,16 @@ SIGNATURES = {
     ),
     "aspec_output_block_layout": (_int, [_c_void_p] + [_i64] * 6 + [_c_void_p] * 3),
     "aspec_qk_norm_rope_fwd": (
-        _int, [_c_void_p] * 7 + [_i64, _i64] + [_c_void_p] * 3 + [_i64] * 6 + [_f32]
+        _int, [_c_void_p] * 7 + [_i64, _i64] + [_c_void_p] * 3 + [_i64] * 6 + [_f32, _int]
         + [_c_void_p] * 6
     ),
     "aspec_qk_norm_rope_bwd_workspace_bytes": (_int, [_i64] * 5 + [_size_p]),
     "aspec_qk_norm_rope_bwd": (
-        _int, [_c_void_p] * 11 + [_i64, _i64] + [_c_void_p] * 3 + [_i64] * 6 + [_f32]
+        _int, [_c_void_p] * 11 + [_i64, _i64] + [_c_void_p] * 3 + [_i64] * 6 + [_f32, _int]
         + [_c_void_p] * 8
     ),
     "aspec_qk_norm_rope_bwd_noalloc": (
-        _int, [_c_void_p] * 11 + [_i64, _i64] + [_c_void_p] * 3 + [_i64] * 6 + [_f32]
+        _int, [_c_void_p] * 11 + [_i64, _i64] + [_c_void_p] * 3 + [_i64] * 6 + [_f32, _int]
         + [_c_void_p] * 7
     ),
     "aspec_rmsnorm_fwd": (_int, [_c_void_p] * 3 + [_i64, _i64, _f32] + [_c_void_p] * 4),
@@ -124,7 +124,7 @@ SIGNATURES = {
     "aspec_pack_work_aware_rows": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3),
 }
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _lock = threading.Lock()
 _lib = None

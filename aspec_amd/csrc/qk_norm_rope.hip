@@ -3,7 +3,7 @@
 // aspec/models/draft/dflash.py:280-327). HBM-bound elementwise work over head rows of 128 dims.
 //
 // Forward, per head row x (one token, one head): rstd = 1/sqrt(mean(x^2) + eps), a = x*rstd*w,
-// out = a*cos[pos] + rotate_half(a)*sin[pos]; all in fp32, rounded once to bf16. Query rows take
+// out = a*cos[pos] + rotate_half(a)*sin[pos]; all in fp32, rounded once to bf16 or fp16. Query rows take
 // the query weight; context and draft key rows take the key weight and land in one joined key
 // tensor [B, Lc + Ld, Hkv, D] (context first).
 // Backward, with g = dL/dout: da = g*cos + rotate_half^T(g*sin), dw += da*n (n = x*rstd),
@@ -86,18 +86,41 @@ __device__ __forceinline__ HeadRow locate(const QkArgs& a, int64_t r) {
   return h;
 }
 
-__device__ __forceinline__ void load4(const uint16_t* p, float (&v)[4]) {
-  const u32x2 w = *reinterpret_cast<const u32x2*>(p);
-  v[0] = __uint_as_float(w.x << 16);
-  v[1] = __uint_as_float(w.x & 0xffff0000u);
-  v[2] = __uint_as_float(w.y << 16);
-  v[3] = __uint_as_float(w.y & 0xffff0000u);
+// Activations, weights and cos/sin are bf16 or fp16 (F16); arithmetic is fp32 and each output is
+// rounded once, to nearest even.
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
+template <bool F16>
+__device__ __forceinline__ void load4(const uint16_t* p, float (&v)[4]) {
+  const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+  if constexpr (F16) {
+    v[0] = f16_to_f32(w.x & 0xffffu);
+    v[1] = f16_to_f32(w.x >> 16);
+    v[2] = f16_to_f32(w.y & 0xffffu);
+    v[3] = f16_to_f32(w.y >> 16);
+  } else {
+    v[0] = __uint_as_float(w.x << 16);
+    v[1] = __uint_as_float(w.x & 0xffff0000u);
+    v[2] = __uint_as_float(w.y << 16);
+    v[3] = __uint_as_float(w.y & 0xffff0000u);
+  }
+}
+
+template <bool F16>
 __device__ __forceinline__ void store4(uint16_t* p, const float (&v)[4]) {
   u32x2 w;
-  w.x = pack_bf16x2(v[0], v[1]);
-  w.y = pack_bf16x2(v[2], v[3]);
+  if constexpr (F16) {
+    w.x = f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16);
+    w.y = f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16);
+  } else {
+    w.x = pack_bf16x2(v[0], v[1]);
+    w.y = pack_bf16x2(v[2], v[3]);
+  }
   *reinterpret_cast<u32x2*>(p) = w;
 }
 
@@ -109,6 +132,7 @@ __device__ __forceinline__ float row_sum(float v) {
 }
 
 // cos / sin of this lane's dims at `pos` (clamped into the table; `bad` when it was outside).
+template <bool F16>
 __device__ __forceinline__ void rope_rows(const QkArgs& a, int64_t pos, int j, float (&cl)[4],
                                           float (&ch)[4], float (&sl)[4], float (&sh)[4],
                                           bool& bad) {
@@ -116,12 +140,13 @@ __device__ __forceinline__ void rope_rows(const QkArgs& a, int64_t pos, int j, f
   const int64_t p = bad ? 0 : pos;
   const uint16_t* c = a.cos + p * a.rope_stride;
   const uint16_t* s = a.sin + p * a.rope_stride;
-  load4(c + 4 * j, cl);
-  load4(c + 64 + 4 * j, ch);
-  load4(s + 4 * j, sl);
-  load4(s + 64 + 4 * j, sh);
+  load4<F16>(c + 4 * j, cl);
+  load4<F16>(c + 64 + 4 * j, ch);
+  load4<F16>(s + 4 * j, sl);
+  load4<F16>(s + 64 + 4 * j, sh);
 }
 
+template <bool F16>
 __global__ void __launch_bounds__(256) qk_norm_rope_fwd_kernel(QkArgs a) {
   const int j = threadIdx.x & 15;
   const int64_t r = static_cast<int64_t>(blockIdx.x) * kRowsPerGroup + (threadIdx.x >> 4);
@@ -131,13 +156,13 @@ __global__ void __launch_bounds__(256) qk_norm_rope_fwd_kernel(QkArgs a) {
   const int64_t* pos = h.seg == 0 ? a.pos_q : h.seg == 1 ? a.pos_ctx : a.pos_draft;
   const uint16_t* w = h.seg == 0 ? a.wq : a.wk;
   float xl[4], xh[4], wl[4], wh[4];
-  load4(src + 4 * j, xl);
-  load4(src + 64 + 4 * j, xh);
-  load4(w + 4 * j, wl);
-  load4(w + 64 + 4 * j, wh);
+  load4<F16>(src + 4 * j, xl);
+  load4<F16>(src + 64 + 4 * j, xh);
+  load4<F16>(w + 4 * j, wl);
+  load4<F16>(w + 64 + 4 * j, wh);
   float cl[4], ch[4], sl[4], sh[4];
   bool bad;
-  rope_rows(a, pos[h.token], j, cl, ch, sl, sh, bad);
+  rope_rows<F16>(a, pos[h.token], j, cl, ch, sl, sh, bad);
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) ss += xl[i] * xl[i] + xh[i] * xh[i];
@@ -151,8 +176,8 @@ __global__ void __launch_bounds__(256) qk_norm_rope_fwd_kernel(QkArgs a) {
     oh[i] = bad ? NAN : ah * ch[i] + al * sh[i];
   }
   uint16_t* dst = (h.seg == 0 ? a.q_out : a.k_out) + h.out;
-  store4(dst + 4 * j, ol);
-  store4(dst + 64 + 4 * j, oh);
+  store4<F16>(dst + 4 * j, ol);
+  store4<F16>(dst + 64 + 4 * j, oh);
   if (j == 0) {
     (h.seg == 0 ? a.rstd_q : a.rstd_k)[h.rstd] = rstd;
     if (bad) atomicOr(a.flags, 1);
@@ -161,6 +186,7 @@ __global__ void __launch_bounds__(256) qk_norm_rope_fwd_kernel(QkArgs a) {
 
 // Grid-strided over 16-row groups; per-lane dw accumulators for both weights, reduced over the
 // workgroup into partials[seg][blockIdx][D].
+template <bool F16>
 __global__ void __launch_bounds__(256) qk_norm_rope_bwd_kernel(QkArgs a) {
   __shared__ float red[2][kRowsPerGroup][kQkDim];
   const int j = threadIdx.x & 15;
@@ -175,15 +201,15 @@ __global__ void __launch_bounds__(256) qk_norm_rope_bwd_kernel(QkArgs a) {
     const int64_t* pos = h.seg == 0 ? a.pos_q : h.seg == 1 ? a.pos_ctx : a.pos_draft;
     const uint16_t* w = h.seg == 0 ? a.wq : a.wk;
     float xl[4], xh[4], gl[4], gh[4], wl[4], wh[4];
-    load4(src + 4 * j, xl);
-    load4(src + 64 + 4 * j, xh);
-    load4(g + 4 * j, gl);
-    load4(g + 64 + 4 * j, gh);
-    load4(w + 4 * j, wl);
-    load4(w + 64 + 4 * j, wh);
+    load4<F16>(src + 4 * j, xl);
+    load4<F16>(src + 64 + 4 * j, xh);
+    load4<F16>(g + 4 * j, gl);
+    load4<F16>(g + 64 + 4 * j, gh);
+    load4<F16>(w + 4 * j, wl);
+    load4<F16>(w + 64 + 4 * j, wh);
     float cl[4], ch[4], sl[4], sh[4];
     bool bad;
-    rope_rows(a, pos[h.token], j, cl, ch, sl, sh, bad);
+    rope_rows<F16>(a, pos[h.token], j, cl, ch, sl, sh, bad);
     const float rstd = (h.seg == 0 ? a.rstd_q : a.rstd_k)[h.rstd];
     float nl[4], nh[4], dnl[4], dnh[4];
     float dot = 0.f;
@@ -213,8 +239,8 @@ __global__ void __launch_bounds__(256) qk_norm_rope_bwd_kernel(QkArgs a) {
       oh[i] = rstd * (dnh[i] - nh[i] * mean);
     }
     uint16_t* dst = (h.seg == 0 ? a.q_out : h.seg == 1 ? a.dctx : a.ddraft) + h.src;
-    store4(dst + 4 * j, ol);
-    store4(dst + 64 + 4 * j, oh);
+    store4<F16>(dst + 4 * j, ol);
+    store4<F16>(dst + 64 + 4 * j, oh);
     if (j == 0 && bad) atomicOr(a.flags, 1);
   }
 #pragma unroll
@@ -249,6 +275,12 @@ __global__ void __launch_bounds__(256) qk_norm_rope_dw_kernel(QkArgs a, int grou
     __syncthreads();
   }
   if (threadIdx.x == 0) (seg == 0 ? a.dwq : a.dwk)[d] = part[0];
+}
+
+int check_dtype(int32_t dtype) {
+  if (dtype != ASPEC_MASK_BF16 && dtype != ASPEC_MASK_F16)
+    return set_error(ASPEC_ERR_UNSUPPORTED, "DSpark Q/K norm+RoPE serves bf16 and fp16 (dtype %d)", dtype);
+  return ASPEC_OK;
 }
 
 int check_sizes(const QkArgs& a, int64_t head_dim) {
@@ -359,9 +391,10 @@ extern "C" int aspec_qk_norm_rope_fwd(const void* query, const void* context_key
                                       const int64_t* context_positions,
                                       const int64_t* draft_positions, int64_t batch,
                                       int64_t context_len, int64_t draft_len, int64_t q_heads,
-                                      int64_t kv_heads, int64_t head_dim, float eps, void* q_out,
-                                      void* k_out, float* rstd_q, float* rstd_k,
+                                      int64_t kv_heads, int64_t head_dim, float eps, int32_t dtype,
+                                      void* q_out, void* k_out, float* rstd_q, float* rstd_k,
                                       int32_t* status_flags, void* stream) {
+  if (int rc0 = check_dtype(dtype)) return rc0;
   QkArgs a = make_args(query, context_key, draft_key, q_weight, k_weight, cos, sin, rope_rows,
                        rope_stride, query_positions, context_positions, draft_positions, batch,
                        context_len, draft_len, q_heads, kv_heads, eps);
@@ -378,8 +411,12 @@ extern "C" int aspec_qk_norm_rope_fwd(const void* query, const void* context_key
   a.rstd_k = rstd_k;
   a.flags = status_flags;
   const int64_t groups = (a.rows_q + a.rows_c + a.rows_d + kRowsPerGroup - 1) / kRowsPerGroup;
-  hipLaunchKernelGGL(qk_norm_rope_fwd_kernel, dim3(static_cast<uint32_t>(groups)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
+  if (dtype == ASPEC_MASK_F16)
+    hipLaunchKernelGGL(qk_norm_rope_fwd_kernel<true>, dim3(static_cast<uint32_t>(groups)), dim3(256),
+                       0, static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_fwd_kernel<false>, dim3(static_cast<uint32_t>(groups)), dim3(256),
+                       0, static_cast<hipStream_t>(stream), a);
   return check_launch("qk_norm_rope_fwd_kernel");
 }
 
@@ -402,9 +439,10 @@ extern "C" int aspec_qk_norm_rope_bwd(
     const void* k_weight, const void* cos, const void* sin, int64_t rope_rows,
     int64_t rope_stride, const int64_t* query_positions, const int64_t* context_positions,
     const int64_t* draft_positions, int64_t batch, int64_t context_len, int64_t draft_len,
-    int64_t q_heads, int64_t kv_heads, int64_t head_dim, float eps, void* d_query,
+    int64_t q_heads, int64_t kv_heads, int64_t head_dim, float eps, int32_t dtype, void* d_query,
     void* d_context_key, void* d_draft_key, float* dw_q, float* dw_k, void* workspace,
     int32_t* status_flags, void* stream) {
+  if (int rc0 = check_dtype(dtype)) return rc0;
   QkArgs a = make_args(query, context_key, draft_key, q_weight, k_weight, cos, sin, rope_rows,
                        rope_stride, query_positions, context_positions, draft_positions, batch,
                        context_len, draft_len, q_heads, kv_heads, eps);
@@ -431,7 +469,10 @@ extern "C" int aspec_qk_norm_rope_bwd(
   a.flags = status_flags;
   const int groups = bwd_groups(a);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(qk_norm_rope_bwd_kernel, dim3(static_cast<uint32_t>(groups)), dim3(256), 0, s, a);
+  if (dtype == ASPEC_MASK_F16)
+    hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<true>, dim3(static_cast<uint32_t>(groups)), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<false>, dim3(static_cast<uint32_t>(groups)), dim3(256), 0, s, a);
   if ((rc = check_launch("qk_norm_rope_bwd_kernel"))) return rc;
   hipLaunchKernelGGL(qk_norm_rope_dw_kernel, dim3(2 * kQkDim), dim3(256), 0, s, a, groups);
   return check_launch("qk_norm_rope_dw_kernel");
@@ -443,7 +484,7 @@ extern "C" int aspec_qk_norm_rope_bwd_noalloc(
     const void* k_weight, const void* cos, const void* sin, int64_t rope_rows,
     int64_t rope_stride, const int64_t* query_positions, const int64_t* context_positions,
     const int64_t* draft_positions, int64_t batch, int64_t context_len, int64_t draft_len,
-    int64_t q_heads, int64_t kv_heads, int64_t head_dim, float eps, void* d_query,
+    int64_t q_heads, int64_t kv_heads, int64_t head_dim, float eps, int32_t dtype, void* d_query,
     void* d_context_key, void* d_draft_key, float* dw_q, float* dw_k, int32_t* status_flags,
     void* stream) {
   size_t need = 0;
@@ -459,6 +500,7 @@ extern "C" int aspec_qk_norm_rope_bwd_noalloc(
   return aspec_qk_norm_rope_bwd(grad_q, grad_k, query, context_key, draft_key, rstd_q, rstd_k,
                                 q_weight, k_weight, cos, sin, rope_rows, rope_stride,
                                 query_positions, context_positions, draft_positions, batch,
-                                context_len, draft_len, q_heads, kv_heads, head_dim, eps, d_query,
-                                d_context_key, d_draft_key, dw_q, dw_k, ptr, status_flags, stream);
+                                context_len, draft_len, q_heads, kv_heads, head_dim, eps, dtype,
+                                d_query, d_context_key, d_draft_key, dw_q, dw_k, ptr, status_flags,
+                                stream);
 }

@@ -71,8 +71,6 @@ class _DSparkQkNormRope(torch.autograd.Function):
             raise ValueError("query, context_key, and draft_key must share one dtype")
         if query_norm_weight.dtype != query.dtype or key_norm_weight.dtype != query.dtype:
             raise ValueError("Q/K norm weights must share the activation dtype")
-        if query.dtype != torch.bfloat16:
-            raise NotImplementedError("the HIP Q/K kernel serves bf16 activations")
         if head_dim != _HEAD_DIM:
             raise NotImplementedError(f"the HIP Q/K kernel serves head_dim {_HEAD_DIM}, got {head_dim}")
 
@@ -115,9 +113,9 @@ class _DSparkQkNormRope(torch.autograd.Function):
                       cos_2d.data_ptr(), sin_2d.data_ptr(), cos_2d.shape[0], cos_2d.stride(0),
                       query_position_ids.data_ptr(), context_position_ids.data_ptr(),
                       draft_position_ids.data_ptr(), batch, context_len, draft_len, num_heads,
-                      num_kv_heads, head_dim, float(variance_epsilon), query_out.data_ptr(),
-                      key_out.data_ptr(), rstd_q.data_ptr(), rstd_k.data_ptr(), flags.data_ptr(),
-                      _lib.stream_handle(dev))
+                      num_kv_heads, head_dim, float(variance_epsilon), _lib.mask_dtype_code(query),
+                      query_out.data_ptr(), key_out.data_ptr(), rstd_q.data_ptr(), rstd_k.data_ptr(),
+                      flags.data_ptr(), _lib.stream_handle(dev))
         global _last_flags
         _last_flags = flags
         ctx.save_for_backward(query, context_key, draft_key, query_norm_weight, key_norm_weight,
@@ -159,7 +157,8 @@ class _DSparkQkNormRope(torch.autograd.Function):
                       key_norm_weight.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
                       cos.stride(0), position_q.data_ptr(), position_context.data_ptr(),
                       position_draft.data_ptr(), batch, context_len, draft_len, num_heads,
-                      num_kv_heads, head_dim, ctx.variance_epsilon, out_query.data_ptr(),
+                      num_kv_heads, head_dim, ctx.variance_epsilon, _lib.mask_dtype_code(query),
+                      out_query.data_ptr(),
                       out_context_key.data_ptr(), out_draft_key.data_ptr(), dw_q.data_ptr(),
                       dw_k.data_ptr(), workspace.data_ptr(), flags.data_ptr(),
                       _lib.stream_handle(dev))

@@ -456,9 +456,11 @@ int aspec_dspark_targets(const int64_t* anchors, const uint8_t* keep, const int6
  * DSpark Q/K preparation, forward: per-head RMSNorm of query and keys, the context/draft key join
  * and indexed RoPE. Replaces `dspark_qk_norm_rope` / `_DSparkQkNormRope.forward`
  * (aspec/models/ops/dspark_qk_norm_rope.py:134-280, run_dspark_qk_norm_rope); the math is
- * `_prepare_dflash_qk` (aspec/models/draft/dflash.py:280-327) in fp32 with one rounding to bf16.
+ * `_prepare_dflash_qk` (aspec/models/draft/dflash.py:280-327) in fp32 with one rounding to the
+ * activation dtype.
  *
- * bf16, head_dim 128: query [batch*draft_len][q_heads][128], context_key [batch*context_len]
+ * dtype ASPEC_MASK_BF16 or ASPEC_MASK_F16 (activations, weights and cos/sin alike; the
+ * reference serves both, dspark_qk_norm_rope.py:169-170), head_dim 128: query [batch*draft_len][q_heads][128], context_key [batch*context_len]
  * [kv_heads][128], draft_key [batch*draft_len][kv_heads][128]; q_weight, k_weight [128];
  * cos, sin [rope_rows][rope_stride] (first 128 columns used); positions int64, one per token.
  * Outputs: q_out like query; k_out [batch][context_len + draft_len][kv_heads][128] (context first);
@@ -471,8 +473,8 @@ int aspec_qk_norm_rope_fwd(const void* query, const void* context_key, const voi
                            const int64_t* query_positions, const int64_t* context_positions,
                            const int64_t* draft_positions, int64_t batch, int64_t context_len,
                            int64_t draft_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-                           float eps, void* q_out, void* k_out, float* rstd_q, float* rstd_k,
-                           int32_t* status_flags, void* stream);
+                           float eps, int32_t dtype, void* q_out, void* k_out, float* rstd_q,
+                           float* rstd_k, int32_t* status_flags, void* stream);
 
 /* Bytes of the backward's workspace (per-workgroup weight-gradient partials). */
 int aspec_qk_norm_rope_bwd_workspace_bytes(int64_t batch, int64_t context_len, int64_t draft_len,
@@ -491,8 +493,9 @@ int aspec_qk_norm_rope_bwd(const void* grad_q, const void* grad_k, const void* q
                            int64_t rope_stride, const int64_t* query_positions,
                            const int64_t* context_positions, const int64_t* draft_positions,
                            int64_t batch, int64_t context_len, int64_t draft_len, int64_t q_heads,
-                           int64_t kv_heads, int64_t head_dim, float eps, void* d_query,
-                           void* d_context_key, void* d_draft_key, float* dw_q, float* dw_k,
+                           int64_t kv_heads, int64_t head_dim, float eps, int32_t dtype,
+                           void* d_query, void* d_context_key, void* d_draft_key, float* dw_q,
+                           float* dw_k,
                            void* workspace, int32_t* status_flags, void* stream);
 
 /*
@@ -513,9 +516,9 @@ int aspec_qk_norm_rope_bwd_noalloc(const void* grad_q, const void* grad_k, const
                                    const int64_t* context_positions,
                                    const int64_t* draft_positions, int64_t batch,
                                    int64_t context_len, int64_t draft_len, int64_t q_heads,
-                                   int64_t kv_heads, int64_t head_dim, float eps, void* d_query,
-                                   void* d_context_key, void* d_draft_key, float* dw_q,
-                                   float* dw_k, int32_t* status_flags, void* stream);
+                                   int64_t kv_heads, int64_t head_dim, float eps, int32_t dtype,
+                                   void* d_query, void* d_context_key, void* d_draft_key,
+                                   float* dw_q, float* dw_k, int32_t* status_flags, void* stream);
 
 /*
  * RMSNorm forward over rows of `hidden` bf16 values (multiple of 8, at most 8192), with an

@@ -5,7 +5,10 @@ context / draft lengths (1,5,3), (1,17,7), (2,5,3), 8 query and 2 KV heads, head
 eps 1e-6, positions drawn from a 67-row cos/sin table of random angles; outputs and input
 gradients within atol = rtol = 2e-2, the fp32 weight gradients (read through the C ABI; autograd
 rounds them to the bf16 weights) within rtol 1e-5 / atol 2e-5, and two backward runs bitwise
-equal. Max-abs and relative-L2 errors are printed for every tensor.
+equal. Max-abs and relative-L2 errors are printed for every tensor. The same cases run with fp16
+activations (the reference's kernel serves bf16 and fp16, dspark_qk_norm_rope.py:169-170; its
+tests run bf16): outputs and input gradients within 2e-3, one fp16 rounding of the fp64 result on
+the same fp16 inputs.
 """
 
 import ctypes
@@ -23,9 +26,9 @@ pytestmark = pytest.mark.gpu
 EPS = 1e-6
 
 
-def _inputs(device, batch, lc, ld, hq=8, hkv=2, positions=67, seed=None):
+def _inputs(device, batch, lc, ld, hq=8, hkv=2, positions=67, seed=None, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed if seed is not None else batch * 10_000 + lc * 100 + ld)
-    bf = torch.bfloat16
+    bf = dtype
     query = torch.randn(batch, ld, hq * 128, generator=g).to(bf)
     ctx = torch.randn(batch, lc, hkv * 128, generator=g).to(bf)
     drf = torch.randn(batch, ld, hkv * 128, generator=g).to(bf)
@@ -59,8 +62,8 @@ def _abi_weight_grads(dev, hq, hkv, gq, gk):
     b, ld = dev["pq"].shape
     lc = dev["pc"].shape[1]
     d = dev["query"].device
-    q_out = torch.empty(b * ld, hq, 128, device=d, dtype=torch.bfloat16)
-    k_out = torch.empty(b * (lc + ld), hkv, 128, device=d, dtype=torch.bfloat16)
+    q_out = torch.empty(b * ld, hq, 128, device=d, dtype=dev["query"].dtype)
+    k_out = torch.empty(b * (lc + ld), hkv, 128, device=d, dtype=dev["query"].dtype)
     rq = torch.empty(b * ld, hq, device=d)
     rk = torch.empty(b * (lc + ld), hkv, device=d)
     flags = torch.zeros(1, dtype=torch.int32, device=d)
@@ -68,7 +71,7 @@ def _abi_weight_grads(dev, hq, hkv, gq, gk):
     cos, sin = dev["cos"], dev["sin"]
     common = (dev["wq"].data_ptr(), dev["wk"].data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
               cos.stride(0), dev["pq"].data_ptr(), dev["pc"].data_ptr(), dev["pd"].data_ptr(), b, lc, ld,
-              hq, hkv, 128, EPS)
+              hq, hkv, 128, EPS, _lib.mask_dtype_code(dev["query"]))
     _lib.call("aspec_qk_norm_rope_fwd", dev["query"].data_ptr(), dev["ctx"].data_ptr(), dev["drf"].data_ptr(),
               *common, q_out.data_ptr(), k_out.data_ptr(), rq.data_ptr(), rk.data_ptr(), flags.data_ptr(),
               stream)
@@ -103,23 +106,27 @@ def _report(name, got, ref, atol, rtol):
     np.testing.assert_allclose(got, ref, atol=atol, rtol=rtol)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 @pytest.mark.parametrize(("batch", "lc", "ld"), [(1, 5, 3), (1, 17, 7), (2, 5, 3)])
-def test_forward_backward_match_oracle_and_are_deterministic(gpu, batch, lc, ld):
+def test_forward_backward_match_oracle_and_are_deterministic(gpu, batch, lc, ld, dtype):
     hq, hkv = 8, 2
-    cpu, dev = _inputs(gpu, batch, lc, ld)
+    tol = 2e-2 if dtype == torch.bfloat16 else 2e-3
+    cpu, dev = _inputs(gpu, batch, lc, ld, dtype=dtype)
     g = torch.Generator().manual_seed(7)
-    gq = torch.randn(batch, ld, hq, 128, generator=g).bfloat16()
-    gk = torch.randn(batch, lc + ld, hkv, 128, generator=g).bfloat16()
+    gq = torch.randn(batch, ld, hq, 128, generator=g).to(dtype)
+    gk = torch.randn(batch, lc + ld, hkv, 128, generator=g).to(dtype)
     q, k, grads = _run(dev, hq, hkv, (gq.to(gpu), gk.to(gpu)))
+    assert q.dtype == dtype and k.dtype == dtype and all(t.dtype == dtype for t in grads)
     args = _oracle(cpu, hq, hkv)
     rq, rk, _, _ = Q.prepare_qk(*args)
-    _report("q", q, rq, 2e-2, 2e-2)
-    _report("k", k, rk, 2e-2, 2e-2)
+    _report("q", q, rq, tol, tol)
+    _report("k", k, rk, tol, tol)
     ref = Q.prepare_qk_grad(*args, gq.double().numpy(), gk.double().numpy())
-    # input gradients, and the weight gradients autograd hands the bf16 weights (rounded to bf16)
-    for name, got, r, tol in zip(("dquery", "dcontext_key", "ddraft_key", "dwq(bf16)", "dwk(bf16)"),
-                                 grads, ref, ((2e-2, 2e-2),) * 5):
-        _report(name, got, r, *tol)
+    # input gradients, and the weight gradients autograd hands the weights (rounded to their dtype;
+    # the bar of the reference's bf16 test for those two)
+    for name, got, r, t in zip(("dquery", "dcontext_key", "ddraft_key", "dwq(act)", "dwk(act)"),
+                               grads, ref, (tol, tol, tol, 2e-2, 2e-2)):
+        _report(name, got, r, t, t)
     # the kernel's fp32 weight gradients, at the reference's bar
     dwq, dwk = _abi_weight_grads(dev, hq, hkv, gq.to(gpu), gk.to(gpu))
     _report("dwq(fp32)", dwq, ref[3], 2e-5, 1e-5)
@@ -176,10 +183,9 @@ def test_unsupported_inputs_fail_closed(gpu):
         dspark_qk_norm_rope(dev["query"].float(), dev["ctx"].float(), dev["drf"].float(), dev["wq"].float(),
                             dev["wk"].float(), EPS, dev["cos"][None, None], dev["sin"][None, None],
                             dev["pq"], dev["pc"], dev["pd"], 8, 2, 128)
-    with pytest.raises(NotImplementedError, match="bf16"):
-        h = lambda x: x.half()  # noqa: E731
-        dspark_qk_norm_rope(h(dev["query"]), h(dev["ctx"]), h(dev["drf"]), h(dev["wq"]), h(dev["wk"]), EPS,
-                            h(dev["cos"])[None, None], h(dev["sin"])[None, None], dev["pq"], dev["pc"],
+    with pytest.raises(ValueError, match="share one dtype"):
+        dspark_qk_norm_rope(dev["query"].half(), dev["ctx"], dev["drf"], dev["wq"], dev["wk"], EPS,
+                            dev["cos"][None, None], dev["sin"][None, None], dev["pq"], dev["pc"],
                             dev["pd"], 8, 2, 128)
     with pytest.raises(ValueError, match="query width"):
         dspark_qk_norm_rope(dev["query"], dev["ctx"], dev["drf"], dev["wq"], dev["wk"], EPS,

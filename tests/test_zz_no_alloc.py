@@ -14,6 +14,7 @@ from aspec_amd import _lib
 pytestmark = pytest.mark.gpu
 
 EPS = 1e-6
+BF16 = 4  # ASPEC_MASK_BF16
 
 
 def _case(device, batch, lc, ld, hq, hkv, seed):
@@ -36,7 +37,7 @@ def _case(device, batch, lc, ld, hq, hkv, seed):
     _lib.call("aspec_qk_norm_rope_fwd", x["query"].data_ptr(), x["ctx"].data_ptr(), x["drf"].data_ptr(),
               x["wq"].data_ptr(), x["wk"].data_ptr(), x["cos"].data_ptr(), x["sin"].data_ptr(), 97, 128,
               x["pq"].data_ptr(), x["pc"].data_ptr(), x["pd"].data_ptr(), batch, lc, ld, hq, hkv, 128, EPS,
-              x["q_out"].data_ptr(), x["k_out"].data_ptr(), x["rstd_q"].data_ptr(), x["rstd_k"].data_ptr(),
+              BF16, x["q_out"].data_ptr(), x["k_out"].data_ptr(), x["rstd_q"].data_ptr(), x["rstd_k"].data_ptr(),
               flags.data_ptr(), stream)
     x["gq"] = rnd(batch * ld, hq, 128)
     x["gk"] = rnd(batch * (lc + ld), hkv, 128)
@@ -56,7 +57,7 @@ def _args_head(x):
     return (x["gq"].data_ptr(), x["gk"].data_ptr(), x["query"].data_ptr(), x["ctx"].data_ptr(),
             x["drf"].data_ptr(), x["rstd_q"].data_ptr(), x["rstd_k"].data_ptr(), x["wq"].data_ptr(),
             x["wk"].data_ptr(), x["cos"].data_ptr(), x["sin"].data_ptr(), 97, 128, x["pq"].data_ptr(),
-            x["pc"].data_ptr(), x["pd"].data_ptr(), batch, lc, ld, hq, hkv, 128, EPS)
+            x["pc"].data_ptr(), x["pd"].data_ptr(), batch, lc, ld, hq, hkv, 128, EPS, BF16)
 
 
 def _with_workspace(x):
