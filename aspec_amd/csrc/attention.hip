@@ -45,7 +45,7 @@ struct AttnArgs {
   const float* dlse;
   float* ws_delta;     // [Hq][Nq] rowsum(dO*O) - dLSE
   float* ws_lse2;      // [Hq][Nq] LSE * log2(e)
-  float* ws_dk;        // [K][Hkv][D] fp32 accumulators of key tiles split over several units
+  float* ws_dk;        // [kMaxChunks][K][Hkv][D] fp32 partials of key tiles split over units
   float* ws_dv;
   uint16_t* dq; int64_t dqst, dqsh;
   uint16_t* dk; int64_t dkst, dksh;
@@ -280,6 +280,16 @@ __device__ __forceinline__ void lds_load16_at(const void* base, uint32_t byte_of
                : "s"(lds_address(lds_wave_base)), "v"(byte_off), "s"(sbase)
                : "memory", "m0");
 }
+__device__ __forceinline__ void lds_load4_at(const void* base, uint32_t byte_off, void* lds_wave_base) {
+  const uint64_t b = reinterpret_cast<uintptr_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
+  const uint64_t sbase = static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+               :
+               : "s"(lds_address(lds_wave_base)), "v"(byte_off), "s"(sbase)
+               : "memory", "m0");
+}
 __device__ __forceinline__ void lds_load4(const void* src, void* lds_wave_base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
                :
@@ -508,33 +518,34 @@ __global__ void __launch_bounds__(256) attn_bwd_pre_kernel(AttnArgs a) {
   }
 }
 
-// Grid: (key tile, kv head) pairs. Zeroes (ZERO) or converts to bf16 the fp32 accumulators of key
-// tiles split over more than one unit; other tiles are written directly by their unit.
-template <bool ZERO>
+// Grid: (key tile, kv head) pairs. For key tiles split over several units, sums the units' fp32
+// partials in chunk order (deterministic) and writes bf16 dK (times the softmax scale) and dV; other
+// tiles were written directly by their unit.
 __global__ void __launch_bounds__(256) attn_bwd_acc_kernel(AttnArgs a) {
   const int hkv = blockIdx.x % a.hkv;
   const int64_t n = blockIdx.x / a.hkv;
-  if (a.plan.b_chunks[n] <= 1) return;
+  const int chunks = a.plan.b_chunks[n];
+  if (chunks <= 1) return;
+  const int64_t slot = a.nk * a.hkv * kHeadDim;
   for (int i = threadIdx.x; i < kBwdTileN * (kHeadDim / 4); i += blockDim.x) {
     const int64_t key = n * kBwdTileN + i / (kHeadDim / 4);
     const int d = (i % (kHeadDim / 4)) * 4;
     if (key >= a.nk) continue;
-    float* pk = a.ws_dk + (key * a.hkv + hkv) * kHeadDim + d;
-    float* pv = a.ws_dv + (key * a.hkv + hkv) * kHeadDim + d;
-    if (ZERO) {
-      *reinterpret_cast<f32x4*>(pk) = f32x4{0.f, 0.f, 0.f, 0.f};
-      *reinterpret_cast<f32x4*>(pv) = f32x4{0.f, 0.f, 0.f, 0.f};
-    } else {
-      const f32x4 k4 = *reinterpret_cast<const f32x4*>(pk);
-      const f32x4 v4 = *reinterpret_cast<const f32x4*>(pv);
-      u32x2 wk, wv;
-      wk.x = pack_bf16x2(k4[0] * a.scale, k4[1] * a.scale);
-      wk.y = pack_bf16x2(k4[2] * a.scale, k4[3] * a.scale);
-      wv.x = pack_bf16x2(v4[0], v4[1]);
-      wv.y = pack_bf16x2(v4[2], v4[3]);
-      *reinterpret_cast<u32x2*>(a.dk + key * a.dkst + hkv * a.dksh + d) = wk;
-      *reinterpret_cast<u32x2*>(a.dv + key * a.dvst + hkv * a.dvsh + d) = wv;
+    const float* pk = a.ws_dk + (key * a.hkv + hkv) * kHeadDim + d;
+    const float* pv = a.ws_dv + (key * a.hkv + hkv) * kHeadDim + d;
+    f32x4 k4 = *reinterpret_cast<const f32x4*>(pk);
+    f32x4 v4 = *reinterpret_cast<const f32x4*>(pv);
+    for (int c = 1; c < chunks; ++c) {
+      k4 += *reinterpret_cast<const f32x4*>(pk + c * slot);
+      v4 += *reinterpret_cast<const f32x4*>(pv + c * slot);
     }
+    u32x2 wk, wv;
+    wk.x = pack_bf16x2(k4[0] * a.scale, k4[1] * a.scale);
+    wk.y = pack_bf16x2(k4[2] * a.scale, k4[3] * a.scale);
+    wv.x = pack_bf16x2(v4[0], v4[1]);
+    wv.y = pack_bf16x2(v4[2], v4[3]);
+    *reinterpret_cast<u32x2*>(a.dk + key * a.dkst + hkv * a.dksh + d) = wk;
+    *reinterpret_cast<u32x2*>(a.dv + key * a.dvst + hkv * a.dvsh + d) = wv;
   }
 }
 
@@ -649,13 +660,16 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
 // Eight waves in two roles share each 32-key slice w = wave % 4:
 //   P waves (0-3):  S = Q K^T (K slice in registers), P = exp2(S*scale*log2e - LSE2) masked,
 //                   P -> LDS, dV += P^T dO;
-//   dS waves (4-7): one iteration behind, dP = dO V^T (V slice in registers), dS = P (dP - delta)
-//                   with P from LDS, dK += dS^T Q.
-// The two waves of a SIMD thus overlap one's softmax VALU work with the other's MFMAs. Q/dO rows
-// and the row scalars cycle through four LDS stages: P waves work on stage i, dS waves on stage
-// i-1, stage i+1 is landing and stage i+2 is being loaded, straight from global memory into LDS
-// (global_load_lds_dwordx4: no staging registers), so every load has two iterations to arrive.
-// One barrier per iteration.
+//   dS waves (4-7): dP = dO V^T (V slice in registers), dS = P (dP - delta) with P from LDS,
+//                   dK += dS^T Q.
+// The two waves of a SIMD thus overlap one's softmax VALU work with the other's MFMAs. Each role
+// finishes stage i-1 at the start of trip i from operands carried in registers over the barrier
+// (the P wave's dV product; the dS wave's dS and dK), then starts stage i (S and P; dP), so that
+// a trip begins with MFMAs instead of every wave waiting on the same burst of LDS reads, and the
+// two waves of a SIMD start with complementary work (MFMAs / VALU). Q/dO rows and the row scalars
+// cycle through four LDS stages: stage i is read during trip i only, stage i+1 is landing and
+// stage i+2 is being loaded, straight from global memory into LDS (global_load_lds_dwordx4: no
+// staging registers), so every load has two iterations to arrive. One barrier per iteration.
 // ---------------------------------------------------------------------------------------------
 template <bool P>
 struct Role {
@@ -663,7 +677,6 @@ struct Role {
 };
 
 constexpr int kDkdvWaves = 2 * kKvWaves;
-static_assert(kBwdChunk <= kWave, "a unit's query tiles are held one per lane");
 constexpr int kDkdvStages = 4;
 
 struct KvStage {
@@ -683,43 +696,85 @@ struct PExchange {
   uint4 p[kKvWaves][2][kWave];
 };
 
-// acc = A x B over the 128-dim reduction: A rows from LDS (all eight k-steps read up front), B
-// from registers.
+// LDS read-ahead (k-steps) of the dK/dV kernel's S and dP chains.
+constexpr int kDkdvAhead = 3;
+
+
+// The first kDkdvAhead k-steps of an S / dP chain's A rows (LDS), read before other work.
 template <typename Operand>
-__device__ __forceinline__ f32x16 mfma_chain_lds_reg(const Operand& ra, const bf16x8 (&b)[8]) {
-  uint4 x[8];
+__device__ __forceinline__ void chain_first(uint4 (&x)[8], const Operand& ra) {
 #pragma unroll
-  for (int ds = 0; ds < 8; ++ds) x[ds] = ra.step(ds);
+  for (int ds = 0; ds < kDkdvAhead; ++ds) x[ds] = ra.step(ds);
+}
+
+// acc = A x B over the 128-dim reduction: A rows from LDS (`x` holds the first kDkdvAhead k-steps,
+// the rest are read kDkdvAhead steps ahead of their MFMA), B from registers.
+template <typename Operand>
+__device__ __forceinline__ f32x16 chain_rest(uint4 (&x)[8], const Operand& ra, const bf16x8 (&b)[8]) {
   f32x16 acc{};
 #pragma unroll
-  for (int ds = 0; ds < 8; ++ds) acc = mfma32(as_bf16x8(x[ds]), b[ds], acc);
+  for (int ds = 0; ds < 8; ++ds) {
+    if (ds + kDkdvAhead < 8) x[ds + kDkdvAhead] = ra.step(ds + kDkdvAhead);
+    acc = mfma32(as_bf16x8(x[ds]), b[ds], acc);
+    ASPEC_STEP_FENCE();
+  }
   return acc;
 }
 
-// acc[d] += A(d, ks) x B[ks] over a 32-row reduction (two k-steps), A read transposed from `tile`
-// (all eight fragments read up front).
-__device__ __forceinline__ void mfma_tr_32(f32x16 (&acc)[4], const uint16_t* tile,
-                                           const TrOffsets& tro, const bf16x8 (&b)[2]) {
-  bf16x8 x[2][4];
+// The transposed fragments of a 32-row stage tile: rows (the reduction) 16*ks .. +15, columns
+// 32*d .. +31.
+__device__ __forceinline__ void read_tr_32(bf16x8 (&f)[2][4], const uint16_t* tile, const TrOffsets& tro) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-    for (int d = 0; d < 4; ++d) x[ks][d] = read_tr_operand(tile, tro, ks * 16, d * 32);
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-    for (int d = 0; d < 4; ++d) acc[d] = mfma32(x[ks][d], b[ks], acc[d]);
+    for (int d = 0; d < 4; ++d) f[ks][d] = read_tr_operand(tile, tro, ks * 16, d * 32);
 }
 
-// P wave: S, masked P (to LDS for the dS wave) and dV += P^T dO for one stage. Rows at or past
-// `valid` hold copies of a real row and get an empty mask. `key_base` is the slice's first key.
-// A fully visible stage (a full tile with all rows real) skips the visibility words and the mask.
+// acc[d] += F[ks][d] x B[ks] over a 32-row reduction, every operand in registers.
+__device__ __forceinline__ void mfma_regs_32(f32x16 (&acc)[4], const bf16x8 (&f)[2][4], const bf16x8 (&b)[2]) {
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) acc[d] = mfma32(f[ks][d], b[ks], acc[d]);
+}
+
+// What each role carries over the barrier from one trip to the next: the operands of the products
+// that finish its previous stage, so that a trip starts with MFMAs from registers instead of
+// waiting on LDS reads that every wave of the workgroup issues at the same moment.
+struct PCarry {   // P wave: P of its previous stage (dV's B operand) and that stage's dO^T fragments
+  bf16x8 p[2];
+  bf16x8 d[2][4];
+};
+struct DsCarry {  // dS wave: dP of its previous stage, that stage's Q^T fragments and delta
+  f32x16 dp;
+  bf16x8 q[2][4];
+  f32x4 delta[4];
+};
+
+// P wave, one trip: dV += P^T dO of the previous stage (carried operands), then, on a live stage:
+// S = Q K^T (K slice in registers), the stage's dO^T fragments (read under the softmax), and
+// P = exp2(S*scale*log2e - LSE2) masked, to LDS for the dS wave and into the carry. Rows at or
+// past `valid` hold copies of a real row and get an empty mask. `key_base` is the slice's first
+// key. A fully visible stage (a full tile with all rows real) skips the visibility words and the
+// mask.
 __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf16x8 (&kf)[8],
-                                            f32x16 (&dvacc)[4], float scale_log2, int w, int valid,
-                                            bool all_visible, int key_base, const RowOffsets& ro,
+                                            f32x16 (&dvacc)[4], PCarry& cy, bool live,
+                                            float scale_log2, int w, int valid, bool all_visible,
+                                            int key_base, const RowOffsets& ro,
                                             const TrOffsets& tro, int lane) {
   const int g = lane >> 5;
   const int c = lane & 31;
+  uint4 x[8];
+  f32x4 l4[4];
+  if (live) {
+    chain_first(x, RowOperandR{s.q, ro});
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) l4[rq] = *reinterpret_cast<const f32x4*>(s.lse2 + rq * 8 + g * 4);
+  }
+  ASPEC_STEP_FENCE();
+  mfma_regs_32(dvacc, cy.d, cy.p);
+  ASPEC_STEP_FENCE();
+  if (!live) return;
   if (!all_visible) {
     if (lane < kBwdTileM) {  // visibility word of row `lane` for this slice
       const uint32_t bits = interval_bits(s.ends[0][lane], s.ends[1][lane], key_base) |
@@ -728,13 +783,9 @@ __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf1
     }
     __builtin_amdgcn_wave_barrier();
   }
-  // The row scalars are read before the S chain, so their latency hides under it; the softmax
-  // then runs as one straight-line block per case (the visibility words, needed only by partial
-  // stages, are read after the chain: holding them across it costs the chain its read-ahead).
-  f32x4 l4[4];
-#pragma unroll
-  for (int rq = 0; rq < 4; ++rq) l4[rq] = *reinterpret_cast<const f32x4*>(s.lse2 + rq * 8 + g * 4);
-  f32x16 sacc = mfma_chain_lds_reg(RowOperandR{s.q, ro}, kf);  // rows: queries, lane: key
+  f32x16 sacc = chain_rest(x, RowOperandR{s.q, ro}, kf);  // rows: queries, lane: key
+  read_tr_32(cy.d, s.dout, tro);
+  ASPEC_STEP_FENCE();
   if (all_visible) {
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq)
@@ -753,34 +804,44 @@ __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf1
         sacc[rq * 4 + j] = __int_as_float(__float_as_int(p) & keep);
       }
   }
-  const bf16x8 pp[2] = {pack_c_half(sacc, 0), pack_c_half(sacc, 8)};
-  px.p[w][0][lane] = __builtin_bit_cast(uint4, pp[0]);
-  px.p[w][1][lane] = __builtin_bit_cast(uint4, pp[1]);
-  mfma_tr_32(dvacc, s.dout, tro, pp);
+  cy.p[0] = pack_c_half(sacc, 0);
+  cy.p[1] = pack_c_half(sacc, 8);
+  px.p[w][0][lane] = __builtin_bit_cast(uint4, cy.p[0]);
+  px.p[w][1][lane] = __builtin_bit_cast(uint4, cy.p[1]);
 }
 
-// dS wave: dP, dS = P (dP - delta) and dK += dS^T Q for one stage. P is the bf16 P the dV product
-// used (dS is rounded to bf16 for the dK product in any case).
+// dS wave, one trip: dS = P (dP - delta) and dK += dS^T Q for the stage of its previous trip (dP,
+// delta and the Q^T fragments carried, P from the P wave's exchange buffer: the bf16 P the dV
+// product used; dS is rounded to bf16 for the dK product in any case); then, on a live stage:
+// dP = dO V^T (V slice in registers) and the stage's Q^T fragments and delta.
 __device__ __forceinline__ void dkdv_ds_step(const KvStage& s, const PExchange& px,
-                                             const bf16x8 (&vf)[8], f32x16 (&dkacc)[4], int w,
-                                             const RowOffsets& ro, const TrOffsets& tro, int lane) {
+                                             const bf16x8 (&vf)[8], f32x16 (&dkacc)[4],
+                                             DsCarry& cy, bool live, int w, const RowOffsets& ro,
+                                             const TrOffsets& tro, int lane) {
   const int g = lane >> 5;
-  f32x16 dp = mfma_chain_lds_reg(RowOperandR{s.dout, ro}, vf);
   const uint4 ph[2] = {px.p[w][0][lane], px.p[w][1][lane]};
+  uint4 x[8];
+  if (live) chain_first(x, RowOperandR{s.dout, ro});
+  ASPEC_STEP_FENCE();
+  f32x16 dp = cy.dp;
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq) {
-    const int r0 = rq * 8 + g * 4;
-    const f32x4 d4 = *reinterpret_cast<const f32x4*>(s.delta + r0);
     const uint4& h = ph[rq >> 1];
     const uint32_t lo = (rq & 1) ? h.z : h.x;
     const uint32_t hi = (rq & 1) ? h.w : h.y;
     const f32x4 p4 = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u),
                       __uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dp[rq * 4 + j] = p4[j] * (dp[rq * 4 + j] - d4[j]);
+    for (int j = 0; j < 4; ++j) dp[rq * 4 + j] = p4[j] * (dp[rq * 4 + j] - cy.delta[rq][j]);
   }
   const bf16x8 dd[2] = {pack_c_half(dp, 0), pack_c_half(dp, 8)};
-  mfma_tr_32(dkacc, s.q, tro, dd);
+  mfma_regs_32(dkacc, cy.q, dd);
+  ASPEC_STEP_FENCE();
+  if (!live) return;
+  cy.dp = chain_rest(x, RowOperandR{s.dout, ro}, vf);
+  read_tr_32(cy.q, s.q, tro);
+#pragma unroll
+  for (int rq = 0; rq < 4; ++rq) cy.delta[rq] = *reinterpret_cast<const f32x4*>(s.delta + rq * 8 + g * 4);
 }
 
 // LDS of the dK/dV kernel: the stage ring and P exchange during the walk, then, for the epilogue,
@@ -793,13 +854,14 @@ struct DkdvShared {
     } walk;
     float out[kKvWaves][kBwdTileM * kHeadDim];
   };
+  int32_t list[kUnitListCap];  // the unit's query tiles (| kFullBit)
 };
 
 // Epilogue of one wave: its 32 keys x 128 dims (C layout: lane = key, registers = dims) pass
 // through the LDS tile `t` (row = key; 16-byte chunk j of row k stored at chunk j ^ k, which keeps
 // both the writes and the row reads bank-conflict free) so that every global write instruction
-// covers one contiguous key row: a bf16 store of the whole row (direct) or two fp32 atomic adds
-// of 64 consecutive dims each (key tiles split over several units).
+// covers one contiguous key row: a bf16 store of the whole row (direct) or an fp32 store of the
+// unit's partial into its own slot (key tiles split over several units; no atomics).
 __device__ __forceinline__ void dkdv_store(const f32x16 (&acc)[4], float* t, int64_t key_first,
                                            int64_t nk, bool direct, uint16_t* dst,
                                            int64_t dst_stride, float* ws, int64_t ws_stride,
@@ -820,15 +882,11 @@ __device__ __forceinline__ void dkdv_store(const f32x16 (&acc)[4], float* t, int
     const int64_t key = key_first + k;
     if (key >= nk) break;
     const float* row = t + k * kHeadDim;
-    if (direct) {
-      const f32x2_t v = *reinterpret_cast<const f32x2_t*>(row + (((lane >> 1) ^ k) << 2) + (lane & 1) * 2);
+    const f32x2_t v = *reinterpret_cast<const f32x2_t*>(row + (((lane >> 1) ^ k) << 2) + (lane & 1) * 2);
+    if (direct)
       *reinterpret_cast<uint32_t*>(dst + key * dst_stride + 2 * lane) = pack_bf16x2(v[0] * mul, v[1] * mul);
-    } else {
-      const float v0 = row[(((lane >> 2) ^ k) << 2) + (lane & 3)];
-      const float v1 = row[(((16 + (lane >> 2)) ^ k) << 2) + (lane & 3)];
-      atomicAdd(ws + key * ws_stride + lane, v0);
-      atomicAdd(ws + key * ws_stride + 64 + lane, v1);
-    }
+    else
+      *reinterpret_cast<f32x2_t*>(ws + key * ws_stride + 2 * lane) = v;
   }
 }
 
@@ -856,14 +914,34 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   const int64_t n = unit >> kUnitChunkBits;
   const int chunk = unit & ((1 << kUnitChunkBits) - 1);
   const int count = __builtin_amdgcn_readfirstlane(a.plan.b_cnt[n]);
-  const int first = chunk * kBwdChunk;
-  const int last = min(count, first + kBwdChunk);
-  const int iters = max(0, last - first) * G;
+  const int chunks = __builtin_amdgcn_readfirstlane(a.plan.b_chunks[n]);
+  const int len = bwd_unit_len(count);
+  const int first = chunk * len;
+  const int ntiles = max(0, min(count, first + len) - first);
+  const int iters = ntiles * G;
   const int32_t* list = a.plan.b_list + n * a.plan.nmb;
   const int64_t key0 = n * kBwdTileN;
-  // The unit's (at most kBwdChunk = 64) query tiles, one per lane, read with readlane in the loop: no memory
-  // access there besides the stage loads.
-  const int my_tile = lane < last - first ? list[first + lane] : 0;  // query tile | kFullBit
+  // The unit's query tiles (| kFullBit) are staged in LDS, then held 128 at a time in two window
+  // registers (lane j: entry wbase + j and wbase + 64 + j) and read with readlane in the loop: no
+  // memory access there besides the stage loads.
+  for (int j = tid; j < ntiles; j += kWave * kDkdvWaves) sh.list[j] = list[first + j];
+  __syncthreads();
+  int wbase = 0;
+  int win0 = lane < ntiles ? sh.list[lane] : 0;
+  int win1 = 64 + lane < ntiles ? sh.list[64 + lane] : 0;
+  auto tile_entry = [&](int t) -> uint32_t {  // wbase <= t < wbase + 128
+    const int r = t - wbase;
+    const int e0 = __builtin_amdgcn_readlane(win0, r & 63);
+    const int e1 = __builtin_amdgcn_readlane(win1, r & 63);
+    return static_cast<uint32_t>(r < 64 ? e0 : e1);
+  };
+  auto advance_window = [&](int t) {  // makes t < wbase + 64
+    if (t - wbase >= 64) {
+      wbase += 64;
+      win0 = win1;
+      win1 = wbase + 64 + lane < ntiles ? sh.list[wbase + 64 + lane] : 0;
+    }
+  };
 
   // This wave's B operand for the whole walk: K (P waves) or V (dS waves) rows of its 32 keys.
   const int64_t key = key0 + w * 32 + c;
@@ -876,48 +954,61 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   const RowOffsets ro(lane);
   const TrOffsets tro(lane);
 
-  // Loads of iteration `it` into a stage. Wave v moves Q and dO rows 4v .. 4v+3 (lane l lands at
-  // physical chunk l % 16 of row 4v + l / 16, so it fetches the logical chunk swizzled there);
-  // rows past the tensor repeat its last row. Waves 0-2 also move the row scalars.
-  const int lrow = wave * 4 + (lane >> 4);
-  const int lcol = ((lane & 15) ^ swz(lrow)) * 8;
-  const bool three_loads = wave < 3;
+  const uint32_t qst2 = static_cast<uint32_t>(a.qst * 2), dost2 = static_cast<uint32_t>(a.dost * 2);
+  // Byte distance of the lanes 32-63 array: lse2 follows delta ([Hq][Nq] each), endpoint row e+1
+  // follows row e.
+  const uint32_t lane_half_ws = lane < 32 ? static_cast<uint32_t>(a.ws_lse2 - a.ws_delta) * 4u : 0u;
+  const uint32_t lane_half_ends = lane < 32 ? 0u : static_cast<uint32_t>(a.nq) * 4u;
   auto row_base = [&](int it, int64_t& q0, int& head, int& valid) {
-    q0 = static_cast<int64_t>(__builtin_amdgcn_readlane(my_tile, it / G) & ~kFullBit) * kBwdTileM;
+    q0 = static_cast<int64_t>(tile_entry(it / G) & ~kFullBit) * kBwdTileM;
     head = hkv * G + it % G;
     valid = static_cast<int>(min<int64_t>(kBwdTileM, a.nq - q0));
   };
+  // Loads of iteration `it` into a stage, issued by the four dS waves only: a wave's vector memory
+  // instructions queue behind every other wave's in the CU's address unit, and P waves, which
+  // carry the longer VALU path (the softmax), then never stall on them (measured: 6% faster than
+  // all eight waves issuing). dS wave lw moves Q and dO rows 8lw .. 8lw+7 (lane l lands at
+  // physical chunk l % 16 of its row, so it fetches the logical chunk swizzled there); rows past
+  // the tensor repeat its last row. dS waves 0-2 also move the row scalars.
+  const int lw = wave - kKvWaves;  // 0..3 for dS waves
+  const int lrow_a = lw * 8 + (lane >> 4), lrow_b = lrow_a + 4;
+  const uint32_t lcol_a2 = static_cast<uint32_t>(((lane & 15) ^ swz(lrow_a)) * 8) * 2u;
+  const uint32_t lcol_b2 = static_cast<uint32_t>(((lane & 15) ^ swz(lrow_b)) * 8) * 2u;
+  const bool five_loads = wave >= kKvWaves && wave < kKvWaves + 3;  // four row loads + scalars
   auto issue = [&](int it, KvStage& sb) {
+    if (p_role) return;
     int64_t q0;
     int head, valid;
     row_base(it, q0, head, valid);
-    const int64_t qr = q0 + min(lrow, valid - 1);
-    lds_load16(a.q + qr * a.qst + head * a.qsh + lcol, sb.q + wave * 4 * kRowLd);
-    lds_load16(a.dout + qr * a.dost + head * a.dosh + lcol, sb.dout + wave * 4 * kRowLd);
-    const int64_t r = q0 + min(lane & 31, valid - 1);
-    const int hi = lane >> 5;
-    if (wave == 0) {  // lanes 0-31: lse2, lanes 32-63: delta
-      lds_load4((hi ? a.ws_delta : a.ws_lse2) + static_cast<int64_t>(head) * a.nq + r, sb.lse2);
-    } else if (wave < 3) {  // endpoints 1,2 (wave 1) and 3,4 (wave 2)
-      const int e = (wave - 1) * 2;
-      lds_load4(a.ends + static_cast<int64_t>(e + hi + 1) * a.nq + r, sb.ends[e]);
+    const uint32_t ra = static_cast<uint32_t>(min(lrow_a, valid - 1));
+    const uint32_t rb = static_cast<uint32_t>(min(lrow_b, valid - 1));
+    const uint16_t* qb = a.q + q0 * a.qst + head * a.qsh;
+    const uint16_t* db = a.dout + q0 * a.dost + head * a.dosh;
+    lds_load16_at(qb, ra * qst2 + lcol_a2, sb.q + lw * 8 * kRowLd);
+    lds_load16_at(qb, rb * qst2 + lcol_b2, sb.q + (lw * 8 + 4) * kRowLd);
+    lds_load16_at(db, ra * dost2 + lcol_a2, sb.dout + lw * 8 * kRowLd);
+    lds_load16_at(db, rb * dost2 + lcol_b2, sb.dout + (lw * 8 + 4) * kRowLd);
+    const uint32_t r4 = static_cast<uint32_t>(min(lane & 31, valid - 1)) * 4u;
+    if (lw == 0) {
+      lds_load4_at(a.ws_delta + static_cast<int64_t>(head) * a.nq + q0, r4 + lane_half_ws, sb.lse2);
+    } else if (lw < 3) {
+      lds_load4_at(a.ends + static_cast<int64_t>(lw * 2 - 1) * a.nq + q0, r4 + lane_half_ends,
+                   sb.ends[(lw - 1) * 2]);
     }
   };
   auto wait_loads = [&](bool ahead) {
+    if (p_role) return;
     if (!ahead) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    else if (three_loads) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2));
+    else if (five_loads) __builtin_amdgcn_s_waitcnt(vmcnt_imm(5));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(4));
   };
-  // The edge trips (dS waves at trip 0, P waves at trip iters) run their step like every other
-  // trip, on zeros: stage 3 and P buffer 1 start zeroed, and the P waves' extra step sees no
-  // visible row. Their contributions are exact zeros, and no accumulator is merged across a
-  // branch inside the walk.
+  // The edge trips (dS waves at trip 0, P waves at trip iters) finish a stage of zeros: the carries
+  // start zeroed and P buffer 1 is zero-filled. Their contributions are exact zeros, and no
+  // accumulator is merged across a branch inside the walk.
   {
-    constexpr int n3 = static_cast<int>(sizeof(KvStage) / 16), np = static_cast<int>(sizeof(PExchange) / 16);
-    static_assert(sizeof(KvStage) % 16 == 0 && sizeof(PExchange) % 16 == 0, "16-byte fills");
-    uint4* z3 = reinterpret_cast<uint4*>(&st3);
+    constexpr int np = static_cast<int>(sizeof(PExchange) / 16);
+    static_assert(sizeof(PExchange) % 16 == 0, "16-byte fills");
     uint4* zp = reinterpret_cast<uint4*>(&px1);
-    for (int i = tid; i < n3; i += kWave * kDkdvWaves) z3[i] = make_uint4(0, 0, 0, 0);
     for (int i = tid; i < np; i += kWave * kDkdvWaves) zp[i] = make_uint4(0, 0, 0, 0);
   }
   if (iters > 0) issue(0, st0);
@@ -925,40 +1016,48 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   wait_loads(iters > 1);
   lds_barrier();
 
-  // Trip i (stage ring position K = i % 4): P waves on stage i, dS waves on stage i-1, loads of
-  // iteration i+2 into stage i+2. Each role runs its own copy of the walk (same trips, same
-  // barriers).
-  auto trip = [&](auto role, int i, KvStage& s_cur, KvStage& s_prv, KvStage& s_ld, PExchange& x_cur,
+  // Trip i (stage ring position i % 4): P waves finish stage i-1 (dV) and compute P of stage i;
+  // dS waves finish stage i-1 (dS, dK) and compute dP of stage i; loads of iteration i+2 go into
+  // stage i+2. Stage i is read only during trip i. Each role runs its own copy of the walk (same
+  // trips, same barriers).
+  PCarry pc{};
+  DsCarry dc{};
+  auto trip = [&](auto role, int i, KvStage& s_cur, KvStage& s_ld, PExchange& x_cur,
                   PExchange& x_prv) {
+    advance_window(i / G);
     const bool ahead = i + 2 < iters;
     if (ahead) issue(i + 2, s_ld);
     TrOffsets tro_t = tro;
     opaque(tro_t.lo);
     opaque(tro_t.hi);
+    const bool live = i < iters;
     if constexpr (decltype(role)::value) {
-      const bool live = i < iters;
       int64_t q0;
       int head, valid;
       row_base(i, q0, head, valid);
-      const bool full = (static_cast<uint32_t>(__builtin_amdgcn_readlane(my_tile, i / G)) & kFullBit) != 0;
-      dkdv_p_step(live ? s_cur : st3, x_cur, kvf, acc, a.scale_log2, w, live ? valid : 0,
-                  live && full && valid == kBwdTileM, static_cast<int>(key0) + w * 32, ro, tro_t,
-                  lane);
+      const bool full = (tile_entry(i / G) & kFullBit) != 0;
+      dkdv_p_step(s_cur, x_cur, kvf, acc, pc, live, a.scale_log2, w, valid,
+                  full && valid == kBwdTileM, static_cast<int>(key0) + w * 32, ro, tro_t, lane);
     } else {
-      dkdv_ds_step(s_prv, x_prv, kvf, acc, w, ro, tro_t, lane);  // trip 0: stage 3 and buffer 1
+      dkdv_ds_step(s_cur, x_prv, kvf, acc, dc, live, w, ro, tro_t, lane);
     }
     wait_loads(ahead);  // this wave's part of stage i+1 has landed
     lds_barrier();
   };
+  // The break tests read the trip count through an empty asm: when G divides the unroll factor the
+  // optimizer would otherwise drop three of them and merge three trips into one block, whose
+  // register allocation spills.
+  int stop = iters;
+  asm volatile("" : "+s"(stop));
   auto walk = [&](auto role) {
     for (int i = 0; i <= iters; i += 4) {
-      trip(role, i, st0, st3, st2, px0, px1);
-      if (i + 1 > iters) break;
-      trip(role, i + 1, st1, st0, st3, px1, px0);
-      if (i + 2 > iters) break;
-      trip(role, i + 2, st2, st1, st0, px0, px1);
-      if (i + 3 > iters) break;
-      trip(role, i + 3, st3, st2, st1, px1, px0);
+      trip(role, i, st0, st2, px0, px1);
+      if (i + 1 > stop) break;
+      trip(role, i + 1, st1, st3, px1, px0);
+      if (i + 2 > stop) break;
+      trip(role, i + 2, st2, st0, px0, px1);
+      if (i + 3 > stop) break;
+      trip(role, i + 3, st3, st1, px1, px0);
     }
   };
   if (p_role)
@@ -966,16 +1065,17 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   else
     walk(Role<false>{});
   // Epilogue in the walk's LDS (every load has landed): P waves (dV) first, then dS waves (dK).
-  const bool direct = a.plan.b_chunks[n] == 1;
+  const bool direct = chunks == 1;
   const int64_t ws_stride = static_cast<int64_t>(a.hkv) * kHeadDim;
+  const int64_t ws_slot = static_cast<int64_t>(chunk) * a.nk * ws_stride + hkv * kHeadDim;
   const int64_t key_first = key0 + w * 32;
   if (p_role)
     dkdv_store(acc, sh.out[w], key_first, a.nk, direct, a.dv + hkv * a.dvsh, a.dvst,
-               a.ws_dv + hkv * kHeadDim, ws_stride, 1.f, lane);
+               a.ws_dv + ws_slot, ws_stride, 1.f, lane);
   lds_barrier();
   if (!p_role)
     dkdv_store(acc, sh.out[w], key_first, a.nk, direct, a.dk + hkv * a.dksh, a.dkst,
-               a.ws_dk + hkv * kHeadDim, ws_stride, a.scale, lane);
+               a.ws_dk + ws_slot, ws_stride, a.scale, lane);
 }
 
 int validate(const AttnArgs& a, int64_t head_dim) {
@@ -990,8 +1090,12 @@ int validate(const AttnArgs& a, int64_t head_dim) {
     return set_error(ASPEC_ERR_UNSUPPORTED, "GQA group %d exceeds %d", a.group, kMaxGroup);
   if ((a.kst > 0 && a.kst >= (1LL << 30) / kBwdTileN) || (a.vst > 0 && a.vst >= (1LL << 30) / kBwdTileN))
     return set_error(ASPEC_ERR_UNSUPPORTED, "K/V token stride too large for 32-bit tile offsets");
+  if ((a.qst > 0 && a.qst >= (1LL << 30) / kBwdTileM) || (a.dost > 0 && a.dost >= (1LL << 30) / kBwdTileM))
+    return set_error(ASPEC_ERR_UNSUPPORTED, "Q/dO token stride too large for 32-bit tile offsets");
   if (a.nk >= (1LL << 31) - kBwdTileN)
     return set_error(ASPEC_ERR_INVALID, "too many keys for int32 tile indexing");
+  if (a.nq * a.hq >= (1LL << 29))
+    return set_error(ASPEC_ERR_UNSUPPORTED, "too many query rows x heads for 32-bit workspace offsets");
   return ASPEC_OK;
 }
 
@@ -1055,7 +1159,8 @@ extern "C" int aspec_dspark_attn_bwd_workspace_bytes(int64_t num_queries, int64_
                                                      size_t* bytes) {
   if (num_queries <= 0 || num_keys <= 0 || q_heads <= 0 || kv_heads <= 0 || !bytes)
     return set_error(ASPEC_ERR_INVALID, "workspace size needs positive sizes");
-  *bytes = static_cast<size_t>(2 * num_queries * q_heads + 2 * num_keys * kv_heads * kHeadDim) *
+  *bytes = static_cast<size_t>(2 * num_queries * q_heads +
+                               2 * static_cast<int64_t>(kMaxChunks) * num_keys * kv_heads * kHeadDim) *
            sizeof(float);
   return ASPEC_OK;
 }
@@ -1102,7 +1207,7 @@ extern "C" int aspec_dspark_attn_bwd_stages(
   a.ws_delta = static_cast<float*>(workspace);
   a.ws_lse2 = a.ws_delta + num_queries * q_heads;
   a.ws_dk = a.ws_lse2 + num_queries * q_heads;
-  a.ws_dv = a.ws_dk + num_keys * kv_heads * kHeadDim;
+  a.ws_dv = a.ws_dk + static_cast<int64_t>(kMaxChunks) * num_keys * kv_heads * kHeadDim;
   a.plan = plan_view(const_cast<void*>(plan), num_queries, num_keys);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 acc_grid(static_cast<uint32_t>(a.plan.nnb * a.hkv));
@@ -1112,8 +1217,6 @@ extern "C" int aspec_dspark_attn_bwd_stages(
     hipLaunchKernelGGL(attn_bwd_pre_kernel, dim3(static_cast<uint32_t>((pre_threads + 255) / 256)),
                        dim3(256), 0, s, a);
     if ((rc = check_launch("attn_bwd_pre_kernel"))) return rc;
-    hipLaunchKernelGGL(attn_bwd_acc_kernel<true>, acc_grid, dim3(256), 0, s, a);
-    if ((rc = check_launch("attn_bwd_acc_kernel<zero>"))) return rc;
   }
   if (stages & 2) {
     const dim3 grid(static_cast<uint32_t>(a.plan.nmf * a.hkv));
@@ -1135,8 +1238,8 @@ extern "C" int aspec_dspark_attn_bwd_stages(
     if ((rc = check_launch("attn_bwd_dkdv_kernel"))) return rc;
   }
   if (stages & 8) {
-    hipLaunchKernelGGL(attn_bwd_acc_kernel<false>, acc_grid, dim3(256), 0, s, a);
-    rc = check_launch("attn_bwd_acc_kernel<finalize>");
+    hipLaunchKernelGGL(attn_bwd_acc_kernel, acc_grid, dim3(256), 0, s, a);
+    rc = check_launch("attn_bwd_acc_kernel");
   }
   return rc;
 }

@@ -12,8 +12,14 @@ constexpr int kFwdTileN = 64;
 // Key-major kernel (dK/dV): tiles of kBwdTileM query rows x kBwdTileN keys.
 constexpr int kBwdTileM = 32;
 constexpr int kBwdTileN = 128;
-// dK/dV work units cover at most this many query tiles of one key tile.
+// dK/dV work units: a key tile seen by more than kBwdChunk query tiles is split into units of
+// max(kBwdChunk, ceil(count / kMaxChunks)) query tiles (the last one shorter), so at most
+// kMaxChunks of them, each writing an fp32 partial into its own slot; the finalize sums the slots
+// in unit order, so dK/dV are deterministic. A unit's list of query tiles (at most kUnitListCap) is
+// staged in LDS.
 constexpr int kBwdChunk = 64;
+constexpr int kMaxChunks = 4;
+constexpr int kUnitListCap = 2048;
 // List entries carry the tile index in the low bits and "full tile" in bit 31.
 constexpr uint32_t kFullBit = 0x80000000u;
 // dK/dV work units are packed as (key tile << kUnitChunkBits) | chunk.
@@ -27,11 +33,22 @@ struct PlanView {
   int32_t* b_classes;
   int32_t* b_cnt;     // [nnb] visible query tiles per key tile
   int32_t* b_list;    // [nnb][nmb] descending query tiles | kFullBit
-  int32_t* b_chunks;  // [nnb] work units of each key tile (>= 1)
+  int32_t* b_chunks;  // [nnb] work units of each key tile (1 .. kMaxChunks)
   int32_t* b_units;   // [max_units] (key tile << kUnitChunkBits | chunk), longest first
   int32_t* b_nunits;  // [1]
   size_t bytes;
 };
+
+// Unit length (query tiles) and unit count of a key tile seen by `count` query tiles. Full
+// kBwdChunk units plus a short remainder while that takes at most kMaxChunks units: the short
+// units, sorted last, fill the tail of the launch.
+__host__ __device__ inline int bwd_unit_len(int count) {
+  const int q = (count + kMaxChunks - 1) / kMaxChunks;
+  return q > kBwdChunk ? q : kBwdChunk;
+}
+__host__ __device__ inline int bwd_chunks(int count) {
+  return count <= 0 ? 1 : (count + bwd_unit_len(count) - 1) / bwd_unit_len(count);
+}
 
 inline PlanView plan_view(void* base, int64_t nq, int64_t nk) {
   PlanView p;
@@ -39,7 +56,7 @@ inline PlanView plan_view(void* base, int64_t nq, int64_t nk) {
   p.nnf = (nk + kFwdTileN - 1) / kFwdTileN;
   p.nmb = (nq + kBwdTileM - 1) / kBwdTileM;
   p.nnb = (nk + kBwdTileN - 1) / kBwdTileN;
-  p.max_units = p.nnb * ((p.nmb + kBwdChunk - 1) / kBwdChunk + 1);
+  p.max_units = p.nnb * kMaxChunks;
   int32_t* cur = static_cast<int32_t*>(base);
   size_t used = 0;
   auto take = [&](int64_t count) {

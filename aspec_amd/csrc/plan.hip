@@ -39,34 +39,42 @@ __global__ void __launch_bounds__(kWave) plan_cols_kernel(PlanView p) {
   }
   if (lane == 0) {
     p.b_cnt[n] = count;
-    p.b_chunks[n] = count > kBwdChunk ? (count + kBwdChunk - 1) / kBwdChunk : 1;
+    p.b_chunks[n] = bwd_chunks(count);
   }
 }
 
-// One workgroup: counting sort of the (key tile, chunk) units by chunk length, longest first.
+// One workgroup: counting sort of the (key tile, chunk) units by unit length, longest first. Lengths
+// up to kBwdChunk have a bin each; longer ones share bins 16 lengths wide (their order within a
+// bin is arbitrary, which only affects load balance).
 constexpr int kUnitThreads = 1024;
-static_assert(kBwdChunk < kUnitThreads, "one thread per histogram bin");
+constexpr int kLenBins = kBwdChunk + 1 + (kUnitListCap - kBwdChunk + 15) / 16;
+static_assert(kLenBins <= kUnitThreads, "one thread per histogram bin");
+
+__device__ __forceinline__ int len_bin(int len) {
+  return len <= kBwdChunk ? len : kBwdChunk + 1 + (len - kBwdChunk - 1) / 16;
+}
 
 __global__ void __launch_bounds__(kUnitThreads) plan_units_kernel(PlanView p) {
-  __shared__ int32_t hist[kBwdChunk + 1];
-  __shared__ int32_t cursor[kBwdChunk + 1];
+  __shared__ int32_t hist[kLenBins];
+  __shared__ int32_t cursor[kLenBins];
   __shared__ int32_t total;
   const int tid = threadIdx.x;
-  if (tid <= kBwdChunk) hist[tid] = 0;
+  if (tid < kLenBins) hist[tid] = 0;
   if (tid == 0) total = 0;
   __syncthreads();
   for (int64_t n = tid; n < p.nnb; n += blockDim.x) {
     const int cnt = p.b_cnt[n];
     const int chunks = p.b_chunks[n];
-    for (int c = 0; c < chunks; ++c) atomicAdd(&hist[min(kBwdChunk, max(0, cnt - c * kBwdChunk))], 1);
+    const int len = bwd_unit_len(cnt);
+    for (int c = 0; c < chunks; ++c) atomicAdd(&hist[len_bin(min(len, max(0, cnt - c * len)))], 1);
     atomicAdd(&total, chunks);
   }
   __syncthreads();
   if (tid == 0) {
     int run = 0;
-    for (int len = kBwdChunk; len >= 0; --len) {
-      cursor[len] = run;
-      run += hist[len];
+    for (int b = kLenBins - 1; b >= 0; --b) {
+      cursor[b] = run;
+      run += hist[b];
     }
     p.b_nunits[0] = total;
   }
@@ -74,9 +82,9 @@ __global__ void __launch_bounds__(kUnitThreads) plan_units_kernel(PlanView p) {
   for (int64_t n = tid; n < p.nnb; n += blockDim.x) {
     const int cnt = p.b_cnt[n];
     const int chunks = p.b_chunks[n];
+    const int len = bwd_unit_len(cnt);
     for (int c = 0; c < chunks; ++c) {
-      const int len = min(kBwdChunk, max(0, cnt - c * kBwdChunk));
-      const int pos = atomicAdd(&cursor[len], 1);
+      const int pos = atomicAdd(&cursor[len_bin(min(len, max(0, cnt - c * len)))], 1);
       p.b_units[pos] = static_cast<int32_t>((n << kUnitChunkBits) | c);
     }
   }
@@ -99,7 +107,7 @@ extern "C" int aspec_dspark_plan_build(const int32_t* endpoints, int64_t num_que
   if (num_queries <= 0 || num_keys <= 0 || !endpoints || !plan)
     return set_error(ASPEC_ERR_INVALID, "plan build needs endpoints, a plan buffer and sizes");
   const PlanView p = plan_view(plan, num_queries, num_keys);
-  if (p.nnb >= (1LL << (31 - kUnitChunkBits)) || (p.nmb + kBwdChunk - 1) / kBwdChunk >= (1LL << kUnitChunkBits))
+  if (p.nnb >= (1LL << (31 - kUnitChunkBits)) || p.nmb > static_cast<int64_t>(kMaxChunks) * kUnitListCap)
     return set_error(ASPEC_ERR_UNSUPPORTED, "attention plan too large (%lld queries, %lld keys)",
                      (long long)num_queries, (long long)num_keys);
   hipStream_t s = static_cast<hipStream_t>(stream);

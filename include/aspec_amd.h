@@ -175,8 +175,9 @@ int aspec_dspark_attn_fwd(const void* q, int64_t q_stride_token, int64_t q_strid
 
 /*
  * Workspace (bytes) needed by aspec_dspark_attn_bwd: per-row delta and log2-scaled LSE
- * ([Hq][Nq] fp32 each) and fp32 dK/dV accumulators ([K][Hkv][128] each) for key tiles whose
- * query list is split over several work units.
+ * ([Hq][Nq] fp32 each) and fp32 dK/dV partials ([4][K][Hkv][128] each: one slot per work unit,
+ * at most 4 units per key tile) for key tiles whose query list is split over several units. Only
+ * the slots of split key tiles are written.
  */
 int aspec_dspark_attn_bwd_workspace_bytes(int64_t num_queries, int64_t num_keys, int64_t q_heads,
                                           int64_t kv_heads, size_t* bytes);
@@ -185,10 +186,11 @@ int aspec_dspark_attn_bwd_workspace_bytes(int64_t num_queries, int64_t num_keys,
  * DSpark attention backward: dQ, dK, dV (bf16) from dO (bf16) and an optional dLSE (fp32 [Hq][Nq],
  * NULL = zero). Replaces FA4's block-sparse backward and `_InternalGQA.backward`
  * (aspec/models/ops/cudnn_gqa_backward.py:128-342): the q heads of one KV group are reduced
- * inside the kernel. dQ is written once per row (deterministic). A key tile whose query list fits
- * one work unit writes its dK/dV rows once (deterministic); a key tile split over several units
- * (long context prefixes) sums its fp32 partials with atomics in arrival order, so those bf16 rows
- * may differ by one rounding step between runs. Same layout rules as the forward.
+ * inside the kernel. Every output is deterministic (bitwise equal across runs): dQ is written once
+ * per row; a key tile whose query list fits one work unit writes its dK/dV rows once; a key tile
+ * split over several units (long context prefixes, at most 4 units) has each unit write its fp32
+ * partial into its own slot, and the finalize sums the slots in unit order (no atomics). Same
+ * layout rules as the forward.
  */
 int aspec_dspark_attn_bwd(const void* q, int64_t q_stride_token, int64_t q_stride_head,
                           const void* k, int64_t k_stride_token, int64_t k_stride_head,
@@ -205,11 +207,10 @@ int aspec_dspark_attn_bwd(const void* q, int64_t q_stride_token, int64_t q_strid
 
 /*
  * The same backward, one stage at a time: `stages` is a bit mask of 1 = prepare
- * (delta = rowsum(dO*O) - dLSE and LSE*log2(e) into the workspace, zeroed split-tile
- * accumulators; the role of the reference's preprocess launch,
- * aspec/kernels/cutedsl/cudnn_gqa/preprocess.py:44-333), 2 = dQ, 4 = dK/dV (the main launch,
- * cudnn_gqa_backward.py:276-296), 8 = finalize (split-tile accumulators to bf16, the role of
- * postprocess.py:38-581). Stages run in that order; a later stage needs the workspace an earlier
+ * (delta = rowsum(dO*O) - dLSE and LSE*log2(e) into the workspace; the role of the reference's
+ * preprocess launch, aspec/kernels/cutedsl/cudnn_gqa/preprocess.py:44-333), 2 = dQ, 4 = dK/dV (the
+ * main launch, cudnn_gqa_backward.py:276-296), 8 = finalize (split-tile partials summed in unit
+ * order to bf16, the role of postprocess.py:38-581). Stages run in that order; a later stage needs the workspace an earlier
  * call prepared on the same stream.
  */
 int aspec_dspark_attn_bwd_stages(int stages, const void* q, int64_t q_stride_token,

@@ -166,9 +166,10 @@ def test_full_size_properties(gpu, make):
 
 def test_backward_stream_overlap_matches_serial(gpu):
     """The backward runs dQ beside dK/dV on a second stream by default; the serial order runs the
-    same kernels on one stream. dQ has no atomics: it must agree bit for bit, over repeated calls at
-    the config-2 geometry. dK/dV rows of key tiles split over several units are summed with fp32
-    atomics in arrival order, so they may differ by one bf16 rounding step between any two runs."""
+    same kernels on one stream. Every output is deterministic: dQ rows are written once, and key
+    tiles split over several work units (the long context prefix at this geometry) sum their fp32
+    partials in unit order. dQ, dK and dV must agree bit for bit over repeated calls at the config-2
+    geometry, in either order."""
     from aspec_amd.direct_cp import backward_overlap, set_backward_overlap
 
     w = W.config2()
@@ -189,12 +190,7 @@ def test_backward_stream_overlap_matches_serial(gpu):
         set_backward_overlap(True)
     assert backward_overlap()
 
-    def one_step_apart(a, b):
-        a, b = a.float(), b.float()
-        bound = 2.0 ** -7 * a.abs() + 2.0 ** -10 * a.abs().max()
-        return bool(torch.all((a - b).abs() <= bound))
-
     pairs = list(zip(grads[False], grads[True])) + [(grads[True][0], grads[True][2])]
     for first, second in pairs:
-        assert torch.equal(first[0], second[0])  # dQ
-        assert one_step_apart(first[1], second[1]) and one_step_apart(first[2], second[2])
+        for a, b in zip(first, second):  # dQ, dK, dV
+            assert torch.equal(a, b)

@@ -35,7 +35,7 @@ def test_size_queries_and_error_codes_without_gpu():
     assert lib.aspec_dspark_plan_bytes(8192, 12288, ctypes.byref(size)) == 0
     assert size.value > 0 and size.value % 256 == 0
     assert lib.aspec_dspark_attn_bwd_workspace_bytes(8192, 12288, 32, 8, ctypes.byref(size)) == 0
-    assert size.value == (2 * 8192 * 32 + 2 * 12288 * 8 * 128) * 4
+    assert size.value == (2 * 8192 * 32 + 2 * 4 * 12288 * 8 * 128) * 4  # delta, lse2; 4 dK/dV partial slots
     assert lib.aspec_loss_stats_floats() == 8
     # invalid geometry is rejected before any launch, with the reference's message
     with pytest.raises(ValueError, match="Invalid THD fixed sparse geometry"):
