@@ -9,9 +9,14 @@ see oracle/__init__.py.
                 `extract_context_feature` (dflash.py:1258-1284) and `final_norm` (dflash.py:1471),
                 with the Q/K preparation of `_prepare_dflash_qk` (dflash.py:296-327) and masked
                 softmax attention over the DSpark visibility (oracle/attention.py).
+  layer_forward_rows  the same layer for a subset of query rows: keys and values of every token,
+                everything else for the chosen rows only (the layer is row-local except for its
+                attention), so a full-size geometry stays affordable on the CPU.
 Pinned by tests/test_oracle_layer.py: constant rows normalise to +-w, finite-difference gradients
 of RMSNorm and SwiGLU, silu's value at 0 and its limits, AdamW's closed-form first step
-(p - lr * g / (|g| + eps) for a fresh state) and its clipping and skip rules.
+(p - lr * g / (|g| + eps) for a fresh state) and its clipping and skip rules; layer_forward by
+zeroed sublayers, single-key routing, gate/up order and a hand-computed residual case;
+layer_forward_rows by equality with layer_forward's rows, values and parameter gradients.
 """
 
 from __future__ import annotations
@@ -142,6 +147,47 @@ def layer_forward(params, target_hidden, draft_ids, context_positions, draft_pos
                                   D ** -0.5, torch.float64)[0] for h in range(hkv)]
     attn = torch.cat(heads, 0).permute(1, 0, 2).reshape(nq, hq * D)
     h = draft + attn @ P["o_proj"].T
+    x2 = _rms(h, P["post_attention_layernorm"], eps)
+    gu = x2 @ P["gate_up_proj"].T
+    f = gu.shape[-1] // 2
+    h = h + (torch.nn.functional.silu(gu[:, :f]) * gu[:, f:]) @ P["down_proj"].T
+    return _rms(h, P["final_norm"], eps)
+
+
+def layer_forward_rows(params, target_hidden, draft_ids, context_positions, draft_positions,
+                       visible_rows, rows, cos, sin, eps, dtype=torch.float64):
+    """`layer_forward` restricted to query rows `rows` (int array): keys and values of every context
+    and draft token, queries, attention, o_proj, MLP and final norm of the chosen rows only.
+    visible_rows [len(rows), T + Nq] bool is the visibility of those rows. Computed in `dtype`;
+    params may be tensors that require gradients (autograd flows into every parameter the chosen
+    rows depend on). Returns [len(rows), H]."""
+    P = {k: (v if isinstance(v, torch.Tensor) else torch.as_tensor(np.asarray(v))).to(dtype)
+         for k, v in params.items()}
+    th = torch.as_tensor(np.asarray(target_hidden)).to(dtype).reshape(-1, P["context_proj"].shape[1])
+    ctx = _rms(th @ P["context_proj"].T, P["context_norm"], eps)
+    ids = torch.as_tensor(np.asarray(draft_ids)).reshape(-1)
+    draft = P["embed_tokens"][ids]
+    x = _rms(draft, P["input_layernorm"], eps)
+    D = P["q_norm"].shape[0]
+    hq = P["q_proj"].shape[0] // D
+    hkv = P["k_proj"].shape[0] // D
+    nq, T = x.shape[0], ctx.shape[0]
+    rows = torch.as_tensor(np.asarray(rows, dtype=np.int64))
+    cos2 = torch.as_tensor(np.asarray(cos)).to(dtype).reshape(-1, D)
+    sin2 = torch.as_tensor(np.asarray(sin)).to(dtype).reshape(-1, D)
+    pos_q = torch.as_tensor(np.asarray(draft_positions)).reshape(-1)
+    pos_k = torch.cat([torch.as_tensor(np.asarray(context_positions)).reshape(-1), pos_q])
+    k = torch.cat([ctx @ P["k_proj"].T, x @ P["k_proj"].T], 0).view(T + nq, hkv, D)
+    v = torch.cat([ctx @ P["v_proj"].T, x @ P["v_proj"].T], 0).view(T + nq, hkv, D)
+    k = _norm_rope(k, P["k_norm"], cos2, sin2, pos_k, eps)
+    xr = x[rows]
+    q = _norm_rope((xr @ P["q_proj"].T).view(len(rows), hq, D), P["q_norm"], cos2, sin2, pos_q[rows], eps)
+    vis = torch.as_tensor(np.asarray(visible_rows), dtype=torch.bool)
+    group = hq // hkv
+    heads = [oattn._group_forward(q[:, h * group:(h + 1) * group].permute(1, 0, 2), k[:, h], v[:, h], vis,
+                                  D ** -0.5, dtype)[0] for h in range(hkv)]
+    attn = torch.cat(heads, 0).permute(1, 0, 2).reshape(len(rows), hq * D)
+    h = draft[rows] + attn @ P["o_proj"].T
     x2 = _rms(h, P["post_attention_layernorm"], eps)
     gu = x2 @ P["gate_up_proj"].T
     f = gu.shape[-1] // 2

@@ -1,7 +1,8 @@
 """The one-layer DSpark training step on the GPU: RMSNorm (with the fused residual add), SwiGLU and
 the fused AdamW against the fp64 oracle (bf16 tolerances stated per test), the composed layer
-and its parameter gradients against the fp64 layer oracle at a reduced geometry, and three full
-steps at the Qwen3-8B geometry (config 5)."""
+and its parameter gradients against the fp64 layer oracle at a reduced geometry and, on sampled
+rows, against the fp32 row-restricted layer oracle at the full Qwen3-8B geometry (config 5), and
+three full steps at that geometry."""
 
 import numpy as np
 import pytest
@@ -25,7 +26,8 @@ def _close(name, got, want, rel_l2, atol_frac):
     got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
     err = np.abs(got - want).max()
     rel = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
-    print(f"{name}: max_abs={err:.3e} rel_l2={rel:.3e}")
+    frac = err / max(np.abs(want).max(), 1e-30)
+    print(f"{name}: max_abs={err:.3e} ({frac:.3e} of the largest value) rel_l2={rel:.3e}")
     assert rel < rel_l2, name
     assert err <= atol_frac * max(np.abs(want).max(), 1e-30), name
 
@@ -129,11 +131,13 @@ def test_layer_forward_and_gradients_match_oracle(gpu):
                            batch["context_positions"].cpu().numpy(), batch["draft_positions"].cpu().numpy(),
                            visible, _np(model.rope_cos), _np(model.rope_sin), model.eps)
     (ref * torch.as_tensor(_np(G.to(hidden.dtype)))).sum().backward()
-    _close("layer hidden", _np(hidden), ref.detach().numpy(), 3e-2, 6e-2)
+    # Measured: hidden rel-L2 5.7e-3 (max error 0.9% of the largest value), parameter gradients
+    # rel-L2 5.6e-3 .. 8.4e-3 (max error <= 1.1%); bars at about twice that.
+    _close("layer hidden", _np(hidden), ref.detach().numpy(), 1.2e-2, 2e-2)
     for n, p in model.named_parameters():
         if not p.requires_grad:
             continue
-        _close(f"grad {n}", _np(p.grad), P[n].grad.numpy(), 5e-2, 0.15)
+        _close(f"grad {n}", _np(p.grad), P[n].grad.numpy(), 1.8e-2, 2.5e-2)
     assert len(names) == len(P)
 
 
@@ -183,3 +187,46 @@ def test_config5_full_geometry_steps(gpu):
     assert all(np.isfinite(losses))
     assert opt.optimizer_steps() == 3
     assert not torch.equal(q0, model.q_proj.detach())
+
+
+def test_config5_full_geometry_layer_rows_and_gradients_match_oracle(gpu):
+    """At the full Qwen3-8B geometry of config 5 (H = 4096, GQA 32/8, FFN 12288, 3 documents of
+    4096 context tokens, 507 anchors x 16): the layer's final-normed hidden states on ~50 sampled
+    query rows (every document, first and last rows, every block offset), and every parameter
+    gradient for an upstream gradient carried by those rows only, against the fp32 row-restricted
+    layer oracle (keys and values of every token; pinned to the dense oracle on the CPU)."""
+    torch.manual_seed(0)
+    model = DSparkDraftLayerModel(device=gpu)
+    w = W.config5()
+    batch = layer_batch(model, w, seed=2)
+    hidden = model(batch["target_hidden"], batch["draft_input_ids"], batch["context_positions"],
+                   batch["draft_positions"], batch["metadata"])
+    H = hidden.shape[-1]
+    nq = hidden.numel() // H
+    rows = np.unique(np.concatenate([np.arange(0, nq, nq // 40), [nq - 1], np.arange(16)]))
+    g = torch.zeros(nq, H, device=gpu)
+    g_rows = torch.randn(len(rows), H, generator=torch.Generator().manual_seed(7))
+    g[torch.as_tensor(rows, device=gpu)] = g_rows.to(gpu)
+    hidden.backward(g.reshape(hidden.shape).to(hidden.dtype))
+
+    f32 = lambda t: t.detach().float().cpu()  # noqa: E731
+    P = {n: f32(p).requires_grad_(p.requires_grad) for n, p in model.named_parameters()}
+    ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
+                       w.block_size, w.sequence_length)
+    vis_rows = M.endpoints_to_dense(ends[:, rows], w.num_keys)
+    ref = ol.layer_forward_rows(P, f32(batch["target_hidden"]), batch["draft_input_ids"].cpu(),
+                                batch["context_positions"].cpu(), batch["draft_positions"].cpu(),
+                                vis_rows, rows, f32(model.rope_cos), f32(model.rope_sin), model.eps,
+                                dtype=torch.float32)
+    (ref * g_rows.to(hidden.dtype).float()).sum().backward()
+    # Measured: hidden rows rel-L2 8.8e-3 (max error 1.0% of the largest value), parameter
+    # gradients rel-L2 8.7e-3 .. 1.2e-2 (max error <= 1.4%); bars at about twice that.
+    _close("config5 hidden rows", _np(hidden.reshape(nq, H)[torch.as_tensor(rows, device=gpu)]),
+           ref.detach().double().numpy(), 1.8e-2, 2.5e-2)
+    checked = 0
+    for n, p in model.named_parameters():
+        if not p.requires_grad or P[n].grad is None:
+            continue
+        _close(f"config5 grad {n}", _np(p.grad), P[n].grad.double().numpy(), 2.5e-2, 3e-2)
+        checked += 1
+    assert checked >= 10

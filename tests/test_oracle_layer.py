@@ -207,3 +207,41 @@ def test_layer_forward_swiglu_gates_with_the_first_half():
     y = 2.0 + 2.0 / (1.0 + math.exp(-1.0)) * down.sum(axis=1)
     want = y / np.sqrt((y * y).mean() + 1e-12)
     np.testing.assert_allclose(out, np.broadcast_to(want, (nq, H)), rtol=1e-12)
+
+
+def test_layer_forward_rows_equals_the_dense_layer_rows_values_and_gradients():
+    """The row-restricted oracle (full-size GPU parity) equals the dense layer oracle on the chosen
+    rows, and with an upstream gradient carried by those rows only, every parameter gradient equals
+    the dense layer's (the other rows contribute nothing). Random visibility with some empty rows,
+    real RoPE tables, non-unit norm weights."""
+    r = _rng(11)
+    H, D, hq, hkv, F, T, nq, V = 32, 8, 4, 2, 48, 12, 10, 30
+    params = _layer_params(H, D, hq, hkv, F, V, scale=0.3, seed=12)
+    for name in ("context_norm", "input_layernorm", "q_norm", "k_norm", "post_attention_layernorm",
+                 "final_norm"):
+        params[name] = 1.0 + 0.2 * r.standard_normal(params[name].shape)
+    th = r.standard_normal((1, T, 3 * H))
+    ids = r.integers(0, V, nq)
+    vis = r.random((nq, T + nq)) < 0.5
+    vis[3] = False  # a row without visible keys
+    ang = np.outer(np.arange(64), 1.0 / (100.0 ** (np.arange(D // 2) / (D // 2))))
+    cos = np.concatenate([np.cos(ang)] * 2, axis=1)
+    sin = np.concatenate([np.sin(ang)] * 2, axis=1)
+    ctx_pos, draft_pos = np.arange(T), r.integers(0, 40, nq)
+    rows = np.array([0, 3, 7, 9])
+    g = r.standard_normal((len(rows), H))
+
+    Pd = {k: torch.tensor(v, requires_grad=True) for k, v in params.items()}
+    dense = ol.layer_forward(Pd, th, ids, ctx_pos, draft_pos, vis, cos, sin, 1e-6)
+    (dense[torch.as_tensor(rows)] * torch.as_tensor(g)).sum().backward()
+    Pr = {k: torch.tensor(v, requires_grad=True) for k, v in params.items()}
+    sub = ol.layer_forward_rows(Pr, th, ids, ctx_pos, draft_pos, vis[rows], rows, cos, sin, 1e-6)
+    (sub * torch.as_tensor(g)).sum().backward()
+
+    np.testing.assert_allclose(sub.detach().numpy(), dense.detach().numpy()[rows], rtol=1e-12, atol=1e-12)
+    for name in params:
+        a, b = Pr[name].grad, Pd[name].grad
+        assert (a is None) == (b is None), name
+        if a is not None:
+            np.testing.assert_allclose(a.numpy(), b.numpy(), rtol=1e-10, atol=1e-12, err_msg=name)
+    assert float(Pd["context_proj"].grad.abs().max()) > 0.0  # the check reaches the key path
