@@ -352,7 +352,7 @@ _REGION_KERNEL = {"attn_fwd": "attn_fwd_kernel<4>", "attn_bwd_dq": "attn_bwd_dq_
                   "loss_fwd": "loss_fwd_persistent<8, false, true>", "loss_bwd": "loss_bwd_rows_kernel",
                   "loss_fused": "loss_fwd_persistent<8, false, true, true>",
                   "head_gemm_fwd": "Custom_Cijk_Alik_Bljk_BBS_BH_MT256x256x64_MI16x16x1_UserArgs_shortname0_gfx950",
-                  "qk_norm_rope_fwd": "qk_norm_rope_fwd_kernel", "qk_norm_rope_bwd": "qk_norm_rope_bwd_kernel"}
+                  "qk_norm_rope_fwd": "qk_norm_rope_fwd_kernel<false>", "qk_norm_rope_bwd": "qk_norm_rope_bwd_kernel<false>"}
 _LIBRARY_REGIONS = ("head_gemm_fwd", "head_gemm_dgrad", "teacher_gemm")
 
 
