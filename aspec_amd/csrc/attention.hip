@@ -929,13 +929,13 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   int wbase = 0;
   int win0 = lane < ntiles ? sh.list[lane] : 0;
   int win1 = 64 + lane < ntiles ? sh.list[64 + lane] : 0;
-  auto tile_entry = [&](int t) -> uint32_t {  // wbase <= t < wbase + 128
+  auto tile_entry = [&](int t) __attribute__((always_inline)) -> uint32_t {  // wbase <= t < wbase + 128
     const int r = t - wbase;
     const int e0 = __builtin_amdgcn_readlane(win0, r & 63);
     const int e1 = __builtin_amdgcn_readlane(win1, r & 63);
     return static_cast<uint32_t>(r < 64 ? e0 : e1);
   };
-  auto advance_window = [&](int t) {  // makes t < wbase + 64
+  auto advance_window = [&](int t) __attribute__((always_inline)) {  // makes t < wbase + 64
     if (t - wbase >= 64) {
       wbase += 64;
       win0 = win1;
@@ -959,48 +959,55 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   // follows row e.
   const uint32_t lane_half_ws = lane < 32 ? static_cast<uint32_t>(a.ws_lse2 - a.ws_delta) * 4u : 0u;
   const uint32_t lane_half_ends = lane < 32 ? 0u : static_cast<uint32_t>(a.nq) * 4u;
-  auto row_base = [&](int it, int64_t& q0, int& head, int& valid) {
+  auto row_base = [&](int it, int64_t& q0, int& head, int& valid) __attribute__((always_inline)) {
     q0 = static_cast<int64_t>(tile_entry(it / G) & ~kFullBit) * kBwdTileM;
     head = hkv * G + it % G;
     valid = static_cast<int>(min<int64_t>(kBwdTileM, a.nq - q0));
   };
-  // Loads of iteration `it` into a stage, issued by the four dS waves only: a wave's vector memory
-  // instructions queue behind every other wave's in the CU's address unit, and P waves, which
-  // carry the longer VALU path (the softmax), then never stall on them (measured: 6% faster than
-  // all eight waves issuing). dS wave lw moves Q and dO rows 8lw .. 8lw+7 (lane l lands at
-  // physical chunk l % 16 of its row, so it fetches the logical chunk swizzled there); rows past
-  // the tensor repeat its last row. dS waves 0-2 also move the row scalars.
-  const int lw = wave - kKvWaves;  // 0..3 for dS waves
-  const int lrow_a = lw * 8 + (lane >> 4), lrow_b = lrow_a + 4;
+  // Loads of iteration `it` into a stage, split by role so that no wave queues behind the whole
+  // stage in the CU's address unit: dS wave w moves Q rows 8w .. 8w+7 (and dS waves 0-2 the row
+  // scalars) at the start of a trip, into the stage two ahead; P wave w moves dO rows 8w .. 8w+7
+  // at the end of its trip, after its softmax, into the stage three ahead (the one read during the
+  // previous trip, free once that trip's barrier has passed), when the dS waves' loads have left
+  // the address unit. Lane l lands at physical chunk l % 16 of its row, so it fetches the logical
+  // chunk swizzled there; rows past the tensor repeat its last row.
+  const int lrow_a = w * 8 + (lane >> 4), lrow_b = lrow_a + 4;
   const uint32_t lcol_a2 = static_cast<uint32_t>(((lane & 15) ^ swz(lrow_a)) * 8) * 2u;
   const uint32_t lcol_b2 = static_cast<uint32_t>(((lane & 15) ^ swz(lrow_b)) * 8) * 2u;
-  const bool five_loads = wave >= kKvWaves && wave < kKvWaves + 3;  // four row loads + scalars
-  auto issue = [&](int it, KvStage& sb) {
-    if (p_role) return;
+  const bool three_loads = !p_role && w < 3;  // two row loads + one scalar load
+  auto issue = [&](int it, KvStage& sb) __attribute__((always_inline)) {
     int64_t q0;
     int head, valid;
     row_base(it, q0, head, valid);
     const uint32_t ra = static_cast<uint32_t>(min(lrow_a, valid - 1));
     const uint32_t rb = static_cast<uint32_t>(min(lrow_b, valid - 1));
-    const uint16_t* qb = a.q + q0 * a.qst + head * a.qsh;
-    const uint16_t* db = a.dout + q0 * a.dost + head * a.dosh;
-    lds_load16_at(qb, ra * qst2 + lcol_a2, sb.q + lw * 8 * kRowLd);
-    lds_load16_at(qb, rb * qst2 + lcol_b2, sb.q + (lw * 8 + 4) * kRowLd);
-    lds_load16_at(db, ra * dost2 + lcol_a2, sb.dout + lw * 8 * kRowLd);
-    lds_load16_at(db, rb * dost2 + lcol_b2, sb.dout + (lw * 8 + 4) * kRowLd);
+    const uint16_t* rb_base = p_role ? a.dout + q0 * a.dost + head * a.dosh
+                                     : a.q + q0 * a.qst + head * a.qsh;
+    const uint32_t st2 = p_role ? dost2 : qst2;
+    uint16_t* dst = (p_role ? sb.dout : sb.q) + w * 8 * kRowLd;
+    lds_load16_at(rb_base, ra * st2 + lcol_a2, dst);
+    lds_load16_at(rb_base, rb * st2 + lcol_b2, dst + 4 * kRowLd);
+    if (p_role) return;
     const uint32_t r4 = static_cast<uint32_t>(min(lane & 31, valid - 1)) * 4u;
-    if (lw == 0) {
+    if (w == 0) {
       lds_load4_at(a.ws_delta + static_cast<int64_t>(head) * a.nq + q0, r4 + lane_half_ws, sb.lse2);
-    } else if (lw < 3) {
-      lds_load4_at(a.ends + static_cast<int64_t>(lw * 2 - 1) * a.nq + q0, r4 + lane_half_ends,
-                   sb.ends[(lw - 1) * 2]);
+    } else if (w < 3) {
+      lds_load4_at(a.ends + static_cast<int64_t>(w * 2 - 1) * a.nq + q0, r4 + lane_half_ends,
+                   sb.ends[(w - 1) * 2]);
     }
   };
-  auto wait_loads = [&](bool ahead) {
-    if (p_role) return;
-    if (!ahead) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    else if (five_loads) __builtin_amdgcn_s_waitcnt(vmcnt_imm(5));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(4));
+  // Before the barrier that ends trip i, this wave's loads of stage i+1 have landed; `later`
+  // counts its stages after i+1 already issued (dS waves: i+2; P waves: i+2 and i+3).
+  auto wait_loads = [&](int later) __attribute__((always_inline)) {
+    if (p_role) {
+      if (later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4));
+      else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2));
+      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    } else {
+      if (later == 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      else if (three_loads) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3));
+      else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2));
+    }
   };
   // The edge trips (dS waves at trip 0, P waves at trip iters) finish a stage of zeros: the carries
   // start zeroed and P buffer 1 is zero-filled. Their contributions are exact zeros, and no
@@ -1013,7 +1020,8 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   }
   if (iters > 0) issue(0, st0);
   if (iters > 1) issue(1, st1);
-  wait_loads(iters > 1);
+  if (p_role && iters > 2) issue(2, st2);
+  wait_loads(p_role ? (iters > 1) + (iters > 2) : (iters > 1));  // stage 0 has landed
   lds_barrier();
 
   // Trip i (stage ring position i % 4): P waves finish stage i-1 (dV) and compute P of stage i;
@@ -1022,11 +1030,10 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   // trips, same barriers).
   PCarry pc{};
   DsCarry dc{};
-  auto trip = [&](auto role, int i, KvStage& s_cur, KvStage& s_ld, PExchange& x_cur,
-                  PExchange& x_prv) {
+  auto trip = [&](auto role, int i, KvStage& s_cur, KvStage& s_ld, KvStage& s_nx,
+                  PExchange& x_cur, PExchange& x_prv) __attribute__((always_inline)) {
     advance_window(i / G);
-    const bool ahead = i + 2 < iters;
-    if (ahead) issue(i + 2, s_ld);
+    if (!p_role && i + 2 < iters) issue(i + 2, s_ld);
     TrOffsets tro_t = tro;
     opaque(tro_t.lo);
     opaque(tro_t.hi);
@@ -1041,7 +1048,8 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
     } else {
       dkdv_ds_step(s_cur, x_prv, kvf, acc, dc, live, w, ro, tro_t, lane);
     }
-    wait_loads(ahead);  // this wave's part of stage i+1 has landed
+    if (p_role && i + 3 < iters) issue(i + 3, s_nx);
+    wait_loads(p_role ? (i + 2 < iters) + (i + 3 < iters) : (i + 2 < iters));
     lds_barrier();
   };
   // The break tests read the trip count through an empty asm: when G divides the unroll factor the
@@ -1049,15 +1057,15 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   // register allocation spills.
   int stop = iters;
   asm volatile("" : "+s"(stop));
-  auto walk = [&](auto role) {
+  auto walk = [&](auto role) __attribute__((always_inline)) {
     for (int i = 0; i <= iters; i += 4) {
-      trip(role, i, st0, st2, px0, px1);
+      trip(role, i, st0, st2, st3, px0, px1);
       if (i + 1 > stop) break;
-      trip(role, i + 1, st1, st3, px1, px0);
+      trip(role, i + 1, st1, st3, st0, px1, px0);
       if (i + 2 > stop) break;
-      trip(role, i + 2, st2, st0, px0, px1);
+      trip(role, i + 2, st2, st0, st1, px0, px1);
       if (i + 3 > stop) break;
-      trip(role, i + 3, st3, st1, px1, px0);
+      trip(role, i + 3, st3, st1, st2, px1, px0);
     }
   };
   if (p_role)

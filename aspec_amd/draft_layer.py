@@ -366,39 +366,23 @@ def dspark_layer_step(model, optimizer, batch, *, ce_alpha=0.1, l1_alpha=0.9):
     draft_input_ids / draft_positions [1, Nq], context_positions [1, T], metadata, and the DSpark
     targets (target_ids, teacher_index, weights as `dspark_targets` returns them).
     Returns (loss, grad_norm) as device tensors."""
-    from .loss import ce_l1_from_logits
+    from .head_loss import selective_head_objective
 
     optimizer.zero_grad()
     with torch.no_grad(), _timing.region("teacher_gemm"):
         teacher = batch["teacher_hidden"].reshape(-1, model.hidden) @ model.lm_head.t()
     hidden = model(batch["target_hidden"], batch["draft_input_ids"], batch["context_positions"],
                    batch["draft_positions"], batch["metadata"])
-    logits = _HeadProjection.apply(hidden, model.lm_head, model.lm_head_t)
     targets = batch["targets"]
-    ce, l1 = ce_l1_from_logits(logits, targets.target_ids.reshape(-1), teacher,
-                               teacher_indices=targets.teacher_index.reshape(-1))
-    w = targets.weights.reshape(-1)
-    # (a_ce sum(w ce) + a_l1 sum(w l1)) / sum(w) with one dot product (fewer launches)
-    loss = torch.dot(torch.add(ce * ce_alpha, l1, alpha=l1_alpha), w) / w.sum().clamp(min=1e-6)
+    # (a_ce sum(w ce) + a_l1 sum(w l1)) / sum(w): the normalised weights go into the fused
+    # vocabulary-GEMM + loss + dlogits pass, which returns the objective itself
+    w = targets.weights.reshape(-1).float()
+    w = w / w.sum().clamp(min=1e-6)
+    loss, _, _ = selective_head_objective(hidden.reshape(-1, model.hidden), model.lm_head,
+                                          targets.target_ids.reshape(-1), teacher,
+                                          ce_weights=w * ce_alpha, l1_weights=w * l1_alpha,
+                                          teacher_indices=targets.teacher_index.reshape(-1),
+                                          weight_t=model.lm_head_t)
     loss.backward()
     norm = optimizer.step()
     return loss.detach(), norm
-
-
-class _HeadProjection(torch.autograd.Function):
-    """hidden @ W^T for the frozen head; the dgrad uses W's transposed copy (TN layout)."""
-
-    @staticmethod
-    def forward(ctx, hidden, weight, weight_t):
-        with _timing.region("head_gemm_fwd"):
-            out = hidden @ weight.t()
-        ctx.save_for_backward(weight_t)
-        return out
-
-    @staticmethod
-    @once_differentiable
-    def backward(ctx, grad):
-        (weight_t,) = ctx.saved_tensors
-        with _timing.region("head_gemm_dgrad"):
-            dh = grad.contiguous() @ weight_t.t()
-        return dh, None, None

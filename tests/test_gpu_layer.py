@@ -109,9 +109,9 @@ def test_fused_adamw_matches_oracle_with_clip_and_skip(gpu):
     assert lrs == [warmup_decay_lr(i, max_lr=1e-2, total_steps=10, warmup_steps=2) for i in range(4)]
 
 
-def _small_model(gpu, seed=0):
+def _small_model(gpu, seed=0, draft_vocab=300):
     return DSparkDraftLayerModel(hidden=256, heads=4, kv_heads=2, head_dim=128, ffn=512, vocab=700,
-                                 draft_vocab=300, max_positions=512, device=gpu, seed=seed)
+                                 draft_vocab=draft_vocab, max_positions=512, device=gpu, seed=seed)
 
 
 def test_layer_forward_and_gradients_match_oracle(gpu):
@@ -141,8 +141,13 @@ def test_layer_forward_and_gradients_match_oracle(gpu):
     assert len(names) == len(P)
 
 
-def test_layer_step_loss_matches_oracle(gpu):
-    model = _small_model(gpu, seed=1)
+@pytest.mark.parametrize("draft_vocab", [304, 300])
+def test_layer_step_loss_and_gradients_match_oracle(gpu, draft_vocab):
+    """The step's loss, every parameter gradient and the pre-clip gradient norm against the fp64
+    oracle (layer oracle + CE/L1 oracle gradients pushed back through the frozen head). A draft
+    vocabulary of 304 runs the fused vocabulary-GEMM + loss + dlogits pass, 300 (not a multiple
+    of 8) the logits-then-loss path."""
+    model = _small_model(gpu, seed=1, draft_vocab=draft_vocab)
     opt = FusedBF16Optimizer(model, lr=1e-3, total_steps=100, warmup_ratio=0.0)
     w = W.from_layout("small", [150, 106], np.array([0, 40, 96, 150, 190]), np.array([0, 0, 0, 1, 1]), 16)
     batch = layer_batch(model, w, seed=6)
@@ -151,10 +156,13 @@ def test_layer_step_loss_matches_oracle(gpu):
     ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
                        w.block_size, w.sequence_length)
     visible = M.endpoints_to_dense(ends, w.num_keys)
-    P = {n: torch.tensor(v) for n, v in params_before.items()}
-    hidden = ol.layer_forward(P, _np(batch["target_hidden"]), batch["draft_input_ids"].cpu().numpy(),
-                              batch["context_positions"].cpu().numpy(), batch["draft_positions"].cpu().numpy(),
-                              visible, _np(model.rope_cos), _np(model.rope_sin), model.eps).numpy()
+    P = {n: torch.tensor(v, requires_grad=p.requires_grad)
+         for (n, v), p in zip(params_before.items(), model.parameters())}
+    hidden_t = ol.layer_forward(P, _np(batch["target_hidden"]), batch["draft_input_ids"].cpu().numpy(),
+                                batch["context_positions"].cpu().numpy(),
+                                batch["draft_positions"].cpu().numpy(), visible, _np(model.rope_cos),
+                                _np(model.rope_sin), model.eps)
+    hidden = hidden_t.detach().numpy()
     head = params_before["lm_head"]
     logits = hidden @ head.T
     teacher = (_np(batch["teacher_hidden"]).reshape(-1, head.shape[1]) @ head.T)
@@ -162,11 +170,32 @@ def test_layer_step_loss_matches_oracle(gpu):
     tgt = t.target_ids.reshape(-1).cpu().numpy()
     tidx = t.teacher_index.reshape(-1).cpu().numpy()
     wts = t.weights.reshape(-1).cpu().numpy().astype(np.float64)
+    y = teacher[np.clip(tidx, 0, None)]
     ce = oloss.cross_entropy(logits, tgt)
-    l1 = oloss.l1(logits, teacher[np.clip(tidx, 0, None)])
-    ref = (0.1 * (ce * wts).sum() + 0.9 * (l1 * wts).sum()) / max(wts.sum(), 1e-6)
-    print(f"layer step loss: got={float(loss):.6f} oracle={ref:.6f} grad_norm={float(norm):.4f}")
-    assert float(loss) == pytest.approx(ref, rel=2e-2)
+    l1 = oloss.l1(logits, y)
+    scale = 1.0 / max(wts.sum(), 1e-6)
+    ref = (0.1 * (ce * wts).sum() + 0.9 * (l1 * wts).sum()) * scale
+    dlogits = (oloss.cross_entropy_grad(logits, tgt, 0.1 * wts * scale)
+               + oloss.l1_grad(logits, y, 0.9 * wts * scale))
+    (hidden_t * torch.as_tensor(dlogits @ head)).sum().backward()
+    ref_norm = np.sqrt(sum((P[n].grad.numpy() ** 2).sum() for n in P if P[n].requires_grad))
+    print(f"layer step loss: got={float(loss):.6f} oracle={ref:.6f} grad_norm={float(norm):.5f} "
+          f"oracle={ref_norm:.5f}")
+    assert float(loss) == pytest.approx(ref, rel=2e-3)
+    assert float(norm) == pytest.approx(ref_norm, rel=1e-2)
+    # Measured: parameter gradients rel-L2 1.3e-2 .. 3.9e-2, max error <= 5.6% of the largest
+    # value; bars at about twice that. They are looser than the layer test's because the L1 term
+    # (weight 0.9) has the gradient p (sign(p - q) - sum p sign(p - q)): wherever p ~ q, the bf16
+    # logits' error flips the sign against the fp64 oracle, and dh = dlogits W sums rows of
+    # dlogits that nearly cancel. The loss and the gradient norm stay within 0.1% / 0.3%.
+    bad = []
+    for n, p in model.named_parameters():
+        if p.requires_grad:
+            try:
+                _close(f"grad {n}", _np(p.grad), P[n].grad.numpy(), 8e-2, 1.2e-1)
+            except AssertionError:
+                bad.append(n)
+    assert not bad, bad
     assert opt.optimizer_steps() == 1
     moved = [n for n, p in model.named_parameters() if p.requires_grad
              and not np.array_equal(_np(p), params_before[n])]
