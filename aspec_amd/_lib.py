@@ -116,6 +116,9 @@ SIGNATURES = {
     "aspec_adamw_step": (
         _int, [_c_void_p] * 5 + [_i64] + [_f32] * 6 + [_c_void_p] * 3
     ),
+    "aspec_adamw_step_segments": (
+        _int, [_c_void_p] * 6 + [_int] + [_f32] * 6 + [_c_void_p] * 3
+    ),
     "aspec_dspark_targets": (
         _int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p] + [_i64] * 5
         + [_c_void_p] * 8
@@ -124,7 +127,7 @@ SIGNATURES = {
     "aspec_pack_work_aware_rows": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3),
 }
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _lock = threading.Lock()
 _lib = None

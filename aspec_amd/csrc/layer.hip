@@ -266,32 +266,78 @@ __global__ void __launch_bounds__(256) swiglu_bwd_kernel(SwiGluArgs a) {
 // ---------------------------------------------------------------------------------------------
 constexpr int kAdamBlocks = 1024;  // norm partials (fixed: deterministic norm)
 
-// Device-side optimizer state: written by the finalize kernel, read by the update kernel.
+constexpr int kMaxGradSegments = 64;
+
+// Device-side optimizer state: written by the finalize kernel, read by the update kernel. Each
+// gradient segment (one parameter, or the whole flat buffer) keeps its own step count, as torch's
+// AdamW keeps one per parameter: a parameter without a gradient in some steps takes its bias
+// corrections from the steps in which it had one.
 struct AdamState {
-  int64_t step;      // completed steps
+  int64_t step;      // completed steps (non-finite steps excluded)
   float coef;        // clip coefficient applied to the gradients
   int32_t skip;      // non-finite gradient norm: this step changes nothing
-  float bc1, bc2s;   // 1 - b1^t and sqrt(1 - b2^t) of the step being taken
+  float bc1, bc2s;   // segment 0's 1 - b1^t and sqrt(1 - b2^t) of the step being taken
   float norm;        // gradient norm before clipping
   float pad[2];
+  int64_t seg_step[kMaxGradSegments];  // steps in which segment s had a gradient
+  float seg_bc1[kMaxGradSegments];     // 1 - b1^t_s of the step being taken
+  float seg_bc2s[kMaxGradSegments];    // sqrt(1 - b2^t_s)
 };
-static_assert(sizeof(AdamState) == 40, "AdamState layout is part of the C ABI");
+static_assert(offsetof(AdamState, norm) == 24 && offsetof(AdamState, seg_step) == 40 &&
+                  sizeof(AdamState) == 40 + 16 * kMaxGradSegments,
+              "AdamState layout is part of the C ABI");
 
-__global__ void __launch_bounds__(256) grad_sumsq_kernel(const uint16_t* g, int64_t n, float* partials) {
+// Where the gradients are: one flat buffer (one segment) or one tensor per parameter, in the
+// parameters' flat order. Segment s covers flat elements [end[s-1], end[s]); ptr[s] is its bf16
+// gradient, or null for a parameter without one (it contributes nothing to the norm and is not
+// updated, as torch's optimizers skip a parameter whose grad is None); bit s of `active` is set
+// iff ptr[s] is not null. Every segment but the last holds a multiple of 8 elements and starts
+// 16-byte aligned, so an 8-element chunk never straddles two segments.
+struct GradTable {
+  int nseg;
+  uint64_t active;
+  int64_t end[kMaxGradSegments];
+  const uint16_t* ptr[kMaxGradSegments];
+};
+
+// The gradient of flat element e (null: none) and its segment, by a uniform scan of the table (a
+// handful of scalar loads and lane selects per 8-element chunk).
+__device__ __forceinline__ const uint16_t* grad_at(const GradTable& t, int64_t e, int& seg) {
+  const uint16_t* p = nullptr;
+  int64_t start = 0;
+  seg = 0;
+  for (int s = 0; s < t.nseg; ++s) {
+    const int64_t end = t.end[s];
+    if (e >= start && e < end) {
+      p = t.ptr[s] ? t.ptr[s] + (e - start) : nullptr;
+      seg = s;
+    }
+    start = end;
+  }
+  return p;
+}
+
+__global__ void __launch_bounds__(256) grad_sumsq_kernel(GradTable g, int64_t n, float* partials) {
   __shared__ float red[4];
   float s = 0.f;
   const int64_t n8 = n >> 3;
-  const uint4* g8 = reinterpret_cast<const uint4*>(g);
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n8;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int seg;
+    const uint16_t* gp = grad_at(g, i << 3, seg);
+    if (!gp) continue;
     float f[8];
-    unpack8(g8[i], f);
+    unpack8(*reinterpret_cast<const uint4*>(gp), f);
 #pragma unroll
     for (int k = 0; k < 8; ++k) s = fmaf(f[k], f[k], s);
   }
   if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
-    const float f = bf16_to_f32(g[(n8 << 3) + threadIdx.x]);
-    s = fmaf(f, f, s);
+    int seg;
+    const uint16_t* gp = grad_at(g, (n8 << 3) + threadIdx.x, seg);
+    if (gp) {
+      const float f = bf16_to_f32(*gp);
+      s = fmaf(f, f, s);
+    }
   }
   s = wave_sum(s);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
@@ -301,23 +347,33 @@ __global__ void __launch_bounds__(256) grad_sumsq_kernel(const uint16_t* g, int6
 
 __global__ void __launch_bounds__(64) adam_finalize_kernel(const float* partials, int nparts,
                                                            float max_norm, float b1, float b2,
+                                                           int nseg, uint64_t active,
                                                            AdamState* st) {
   // fixed-order fp64 sum of the partials (one wave, lane-strided then a tree)
   double s = 0.0;
   for (int i = threadIdx.x; i < nparts; i += 64) s += static_cast<double>(partials[i]);
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-  if (threadIdx.x == 0) {
-    const float norm = static_cast<float>(sqrt(s));
+  const float norm = static_cast<float>(sqrt(s));
+  const bool finite = isfinite(norm);
+  // lane j: segment j's step count and bias corrections
+  const int j = threadIdx.x;
+  if (j < nseg) {
+    const int64_t t = st->seg_step[j] + ((finite && ((active >> j) & 1)) ? 1 : 0);
+    st->seg_step[j] = t;
+    st->seg_bc1[j] = static_cast<float>(1.0 - pow(static_cast<double>(b1), static_cast<double>(t)));
+    st->seg_bc2s[j] = static_cast<float>(sqrt(1.0 - pow(static_cast<double>(b2), static_cast<double>(t))));
+    if (j == 0) {
+      st->bc1 = st->seg_bc1[0];
+      st->bc2s = st->seg_bc2s[0];
+    }
+  }
+  if (j == 0) {
     st->norm = norm;
-    const bool finite = isfinite(norm);
     st->skip = finite ? 0 : 1;
     float coef = 1.f;
     if (max_norm > 0.f) coef = fminf(max_norm / (norm + 1e-6f), 1.f);
     st->coef = coef;
-    const int64_t t = st->step + (finite ? 1 : 0);
-    st->step = t;
-    st->bc1 = static_cast<float>(1.0 - pow(static_cast<double>(b1), static_cast<double>(t)));
-    st->bc2s = static_cast<float>(sqrt(1.0 - pow(static_cast<double>(b2), static_cast<double>(t))));
+    st->step += finite ? 1 : 0;
   }
 }
 
@@ -326,7 +382,7 @@ struct AdamArgs {
   float* master;
   float* m;
   float* v;
-  const uint16_t* grad;
+  GradTable grad;
   int64_t n;
   float lr, wd, b1, b2, eps;
   const AdamState* st;
@@ -343,15 +399,19 @@ __device__ __forceinline__ float adam_one(float g, float& p, float& m, float& v,
 
 // Eight parameters per thread and iteration (16-byte bf16, 2 x 16-byte fp32 accesses), scalar tail.
 __global__ void __launch_bounds__(256) adam_update_kernel(AdamArgs a) {
-  const AdamState st = *a.st;
-  if (st.skip) return;
-  const float step_size = a.lr / st.bc1;
+  const float coef = a.st->coef;
+  if (a.st->skip) return;
   const float decay = 1.f - a.lr * a.wd;
   const int64_t n8 = a.n >> 3;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n8; i += stride) {
+    int seg;
+    const uint16_t* gp = grad_at(a.grad, i << 3, seg);
+    if (!gp) continue;
+    const float step_size = a.lr / a.st->seg_bc1[seg];
+    const float bc2s = a.st->seg_bc2s[seg];
     float g[8];
-    unpack8(reinterpret_cast<const uint4*>(a.grad)[i], g);
+    unpack8(*reinterpret_cast<const uint4*>(gp), g);
     f32x4* mp = reinterpret_cast<f32x4*>(a.master) + 2 * i;
     f32x4* mm = reinterpret_cast<f32x4*>(a.m) + 2 * i;
     f32x4* mv = reinterpret_cast<f32x4*>(a.v) + 2 * i;
@@ -362,7 +422,7 @@ __global__ void __launch_bounds__(256) adam_update_kernel(AdamArgs a) {
       p[k] = p4[k >> 2][k & 3];
       m[k] = m4[k >> 2][k & 3];
       v[k] = v4[k >> 2][k & 3];
-      adam_one(g[k] * st.coef, p[k], m[k], v[k], a, step_size, decay, st.bc2s);
+      adam_one(g[k] * coef, p[k], m[k], v[k], a, step_size, decay, bc2s);
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -373,8 +433,12 @@ __global__ void __launch_bounds__(256) adam_update_kernel(AdamArgs a) {
     reinterpret_cast<uint4*>(a.param)[i] = pack8(p);
   }
   for (int64_t i = (n8 << 3) + static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.n; i += stride) {
+    int seg;
+    const uint16_t* gp = grad_at(a.grad, i, seg);
+    if (!gp) continue;
+    const float step_size = a.lr / a.st->seg_bc1[seg];
     float p = a.master[i], m = a.m[i], v = a.v[i];
-    adam_one(bf16_to_f32(a.grad[i]) * st.coef, p, m, v, a, step_size, decay, st.bc2s);
+    adam_one(bf16_to_f32(*gp) * coef, p, m, v, a, step_size, decay, a.st->seg_bc2s[seg]);
     a.master[i] = p;
     a.m[i] = m;
     a.v[i] = v;
@@ -506,14 +570,15 @@ extern "C" int aspec_adamw_workspace_bytes(size_t* bytes) {
   return ASPEC_OK;
 }
 
-extern "C" int aspec_adamw_step(void* params, float* master, float* exp_avg, float* exp_avg_sq,
-                                const void* grads, int64_t n, float lr, float weight_decay,
-                                float beta1, float beta2, float eps, float max_grad_norm,
-                                void* state, void* workspace, void* stream) {
-  if (n <= 0) return set_error(ASPEC_ERR_INVALID, "AdamW needs a positive parameter count");
-  if (!params || !master || !exp_avg || !exp_avg_sq || !grads || !state || !workspace)
+namespace {
+
+int adamw_launch(void* params, float* master, float* exp_avg, float* exp_avg_sq,
+                 const GradTable& table, int64_t n, float lr, float weight_decay, float beta1,
+                 float beta2, float eps, float max_grad_norm, void* state, void* workspace,
+                 void* stream) {
+  if (!params || !master || !exp_avg || !exp_avg_sq || !state || !workspace)
     return set_error(ASPEC_ERR_INVALID, "null pointer passed to AdamW");
-  const void* bufs[] = {params, master, exp_avg, exp_avg_sq, grads};
+  const void* bufs[] = {params, master, exp_avg, exp_avg_sq};
   for (const void* b : bufs)
     if (reinterpret_cast<uintptr_t>(b) & 15)
       return set_error(ASPEC_ERR_INVALID, "AdamW buffers must be 16-byte aligned");
@@ -522,19 +587,18 @@ extern "C" int aspec_adamw_step(void* params, float* master, float* exp_avg, flo
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* partials = static_cast<float*>(workspace);
   AdamState* st = static_cast<AdamState*>(state);
-  hipLaunchKernelGGL(grad_sumsq_kernel, dim3(kAdamBlocks), dim3(256), 0, s,
-                     static_cast<const uint16_t*>(grads), n, partials);
+  hipLaunchKernelGGL(grad_sumsq_kernel, dim3(kAdamBlocks), dim3(256), 0, s, table, n, partials);
   int rc = check_launch("grad_sumsq_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(adam_finalize_kernel, dim3(1), dim3(64), 0, s, static_cast<const float*>(partials),
-                     kAdamBlocks, max_grad_norm, beta1, beta2, st);
+                     kAdamBlocks, max_grad_norm, beta1, beta2, table.nseg, table.active, st);
   if ((rc = check_launch("adam_finalize_kernel"))) return rc;
   AdamArgs a = {};
   a.param = static_cast<uint16_t*>(params);
   a.master = master;
   a.m = exp_avg;
   a.v = exp_avg_sq;
-  a.grad = static_cast<const uint16_t*>(grads);
+  a.grad = table;
   a.n = n;
   a.lr = lr;
   a.wd = weight_decay;
@@ -545,4 +609,54 @@ extern "C" int aspec_adamw_step(void* params, float* master, float* exp_avg, flo
   const dim3 grid(static_cast<uint32_t>(std::min<int64_t>((n / 8 + 255) / 256 + 1, 256 * 16)));
   hipLaunchKernelGGL(adam_update_kernel, grid, dim3(256), 0, s, a);
   return check_launch("adam_update_kernel");
+}
+
+}  // namespace
+
+extern "C" int aspec_adamw_step(void* params, float* master, float* exp_avg, float* exp_avg_sq,
+                                const void* grads, int64_t n, float lr, float weight_decay,
+                                float beta1, float beta2, float eps, float max_grad_norm,
+                                void* state, void* workspace, void* stream) {
+  if (n <= 0) return set_error(ASPEC_ERR_INVALID, "AdamW needs a positive parameter count");
+  if (!grads) return set_error(ASPEC_ERR_INVALID, "null pointer passed to AdamW");
+  if (reinterpret_cast<uintptr_t>(grads) & 15)
+    return set_error(ASPEC_ERR_INVALID, "AdamW buffers must be 16-byte aligned");
+  GradTable t = {};
+  t.nseg = 1;
+  t.active = 1;
+  t.end[0] = n;
+  t.ptr[0] = static_cast<const uint16_t*>(grads);
+  return adamw_launch(params, master, exp_avg, exp_avg_sq, t, n, lr, weight_decay, beta1, beta2,
+                      eps, max_grad_norm, state, workspace, stream);
+}
+
+extern "C" int aspec_adamw_step_segments(void* params, float* master, float* exp_avg,
+                                         float* exp_avg_sq, const void* const* seg_grads,
+                                         const int64_t* seg_numel, int nseg, float lr,
+                                         float weight_decay, float beta1, float beta2, float eps,
+                                         float max_grad_norm, void* state, void* workspace,
+                                         void* stream) {
+  if (!seg_grads || !seg_numel) return set_error(ASPEC_ERR_INVALID, "null segment table passed to AdamW");
+  if (nseg <= 0 || nseg > kMaxGradSegments)
+    return set_error(ASPEC_ERR_UNSUPPORTED, "AdamW segment count must lie in [1, %d], got %d",
+                     kMaxGradSegments, nseg);
+  GradTable t = {};
+  t.nseg = nseg;
+  int64_t n = 0;
+  for (int i = 0; i < nseg; ++i) {
+    if (seg_numel[i] <= 0)
+      return set_error(ASPEC_ERR_INVALID, "AdamW segment %d has no elements", i);
+    if (i + 1 < nseg && (seg_numel[i] & 7))
+      return set_error(ASPEC_ERR_INVALID,
+                       "AdamW segment %d holds %lld elements: every segment but the last must hold "
+                       "a multiple of 8", i, static_cast<long long>(seg_numel[i]));
+    if (reinterpret_cast<uintptr_t>(seg_grads[i]) & 15)
+      return set_error(ASPEC_ERR_INVALID, "AdamW segment %d gradient must be 16-byte aligned", i);
+    n += seg_numel[i];
+    t.end[i] = n;
+    t.ptr[i] = static_cast<const uint16_t*>(seg_grads[i]);
+    if (seg_grads[i]) t.active |= 1ull << i;
+  }
+  return adamw_launch(params, master, exp_avg, exp_avg_sq, t, n, lr, weight_decay, beta1, beta2,
+                      eps, max_grad_norm, state, workspace, stream);
 }

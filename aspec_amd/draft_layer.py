@@ -19,8 +19,9 @@ and the reference's optimizer (`BF16Optimizer`, aspec/training/optimizer.py:40-1
 MI355X-specific layout: the residual adds are fused into the following RMSNorm (one pass writes
 the sum and its normalisation), gate and up are one [2F, H] weight and one GEMM feeding the SwiGLU
 kernel, and the optimizer keeps every trainable parameter as a view of one flat bf16 buffer with
-flat fp32 master / moment buffers and a flat bf16 gradient buffer, updated by one fused kernel
-pass with the clip norm and the skip decision on the device.
+flat fp32 master / moment buffers, updated by one fused kernel pass that reads each gradient where
+autograd left it (a table of per-parameter segments), with the clip norm and the skip decision on
+the device.
 """
 
 from __future__ import annotations
@@ -236,10 +237,15 @@ def warmup_decay_lr(step, *, max_lr, total_steps, warmup_steps=0, min_lr=0.0, in
 
 class FusedBF16Optimizer:
     """`BF16Optimizer` (aspec/training/optimizer.py:40-164) as one fused HIP pass: bf16 model
-    parameters become views of one flat buffer with fp32 master weights and moments; their
-    gradients accumulate into one flat bf16 buffer. `step()` clips to max_grad_norm, skips a
-    non-finite step, applies AdamW (torch's fused semantics) and refreshes the bf16 weights;
-    it returns the pre-clip gradient norm as a device scalar (no host synchronization)."""
+    parameters become views of one flat buffer with fp32 master weights and moments. `step()` reads
+    each gradient where autograd left it (one segment per parameter; a parameter whose grad is None
+    is skipped, as torch's optimizers do), clips to max_grad_norm, skips a non-finite step, applies
+    AdamW (torch's fused semantics, one step count per parameter) and refreshes the bf16 weights;
+    it returns the pre-clip gradient norm as a device scalar (no host synchronization) and, as the
+    reference's step does, leaves every grad None. `zero_grad(set_to_none=False)` instead keeps every gradient as a view of one flat bf16 buffer
+    that autograd accumulates into. With more than 64 trainable parameters, or one whose size is
+    not a multiple of 8, the gradients are gathered into that buffer and a grad of None counts as
+    zeros."""
 
     def __init__(self, model, lr, weight_decay=0.0, max_grad_norm=0.5, total_steps=800_000,
                  warmup_ratio=0.015, decay_style="cosine", min_lr=0.0, betas=(0.9, 0.999), eps=1e-8):
@@ -250,17 +256,17 @@ class FusedBF16Optimizer:
         if any(p.dtype != torch.bfloat16 or p.device != dev for p in self.params):
             raise ValueError("the fused optimizer serves bf16 parameters on one device")
         self.numel = sum(p.numel() for p in self.params)
-        pad = (-self.numel) % 8
-        self.flat = torch.empty(self.numel + pad, dtype=torch.bfloat16, device=dev)
-        self.grads = torch.zeros(self.numel + pad, dtype=torch.bfloat16, device=dev)
+        self._pad = (-self.numel) % 8
+        self.flat = torch.empty(self.numel + self._pad, dtype=torch.bfloat16, device=dev)
+        self._grads = None  # the flat gradient buffer, made on first use
         off = 0
         for p in self.params:
             n = p.numel()
             self.flat[off:off + n].copy_(p.detach().reshape(-1))
             p.data = self.flat[off:off + n].view_as(p)
-            p.grad = self.grads[off:off + n].view_as(p)
+            p.grad = None
             off += n
-        if pad:
+        if self._pad:
             self.flat[self.numel:].zero_()
         self.master = self.flat.float()
         self.exp_avg = torch.zeros_like(self.master)
@@ -275,12 +281,25 @@ class FusedBF16Optimizer:
                              warmup_steps=int(warmup_ratio * total_steps), min_lr=min_lr,
                              decay_style=decay_style)
         self.last_step = 0  # scheduler position (advances every step, as the reference's does)
+        numel = [p.numel() for p in self.params]
+        self._seg_numel = (ctypes.c_int64 * len(numel))(*numel)
+        self._segments_ok = len(numel) <= 64 and all(n % 8 == 0 for n in numel[:-1])
+
+    @property
+    def grads(self):
+        """The flat bf16 gradient buffer (zeroed when first made)."""
+        if self._grads is None:
+            self._grads = torch.zeros(self.numel + self._pad, dtype=torch.bfloat16, device=self.flat.device)
+        return self._grads
 
     def get_learning_rate(self):
         return warmup_decay_lr(self.last_step, **self.schedule)
 
     def zero_grad(self, set_to_none=True):
-        del set_to_none  # the gradient views are kept: autograd accumulates into them in place
+        if set_to_none:
+            for p in self.params:
+                p.grad = None
+            return
         self.grads.zero_()
         for p, off in zip(self.params, self._offsets()):
             if p.grad is None or p.grad.data_ptr() != self.grads[off:].data_ptr():
@@ -292,21 +311,50 @@ class FusedBF16Optimizer:
             yield off
             off += p.numel()
 
+    def _segment_grads(self):
+        """Device pointers of the gradients, one segment per parameter (0 for a grad of None); a
+        gradient that is not a contiguous, 16-byte aligned bf16 tensor of the parameter's shape is
+        first copied into the parameter's slice of the flat gradient buffer."""
+        ptrs = []
+        for p, off in zip(self.params, self._offsets()):
+            g = p.grad
+            if g is None:
+                ptrs.append(0)
+            elif (g.dtype == torch.bfloat16 and g.device == p.device and g.shape == p.shape
+                  and g.is_contiguous() and g.data_ptr() % 16 == 0):
+                ptrs.append(g.data_ptr())
+            else:
+                view = self.grads[off:off + p.numel()].view_as(p)
+                view.copy_(g)
+                ptrs.append(view.data_ptr())
+        return (ctypes.c_void_p * len(ptrs))(*ptrs)
+
     def step(self, closure=None):
         del closure
-        for p, off in zip(self.params, self._offsets()):
-            if p.grad is not None and p.grad.data_ptr() != self.grads[off:].data_ptr():
-                self.grads[off:off + p.numel()].view_as(p).copy_(p.grad)  # a replaced gradient
-                p.grad = self.grads[off:off + p.numel()].view_as(p)
         lr = self.get_learning_rate()
+        args = (float(lr), float(self.weight_decay), float(self.betas[0]), float(self.betas[1]),
+                float(self.eps), float(self.max_grad_norm), _lib.ptr(self.state),
+                _lib.ptr(self.workspace), _lib.stream_handle(self.flat.device))
         with _timing.region("adamw_step"):
-            _lib.call("aspec_adamw_step", _lib.ptr(self.flat), _lib.ptr(self.master),
-                      _lib.ptr(self.exp_avg), _lib.ptr(self.exp_avg_sq), _lib.ptr(self.grads),
-                      self.flat.numel(), float(lr), float(self.weight_decay), float(self.betas[0]),
-                      float(self.betas[1]), float(self.eps), float(self.max_grad_norm),
-                      _lib.ptr(self.state), _lib.ptr(self.workspace),
-                      _lib.stream_handle(self.flat.device))
+            if self._segments_ok:
+                _lib.call("aspec_adamw_step_segments", _lib.ptr(self.flat), _lib.ptr(self.master),
+                          _lib.ptr(self.exp_avg), _lib.ptr(self.exp_avg_sq), self._segment_grads(),
+                          self._seg_numel, len(self.params), *args)
+            else:
+                # more than 64 parameters, or one whose size is not a multiple of 8: every gradient
+                # is gathered into the flat buffer (a grad of None counts as zeros there)
+                for p, off in zip(self.params, self._offsets()):
+                    view = self.grads[off:off + p.numel()].view_as(p)
+                    if p.grad is None:
+                        view.zero_()
+                    elif p.grad.data_ptr() != view.data_ptr():
+                        view.copy_(p.grad)
+                _lib.call("aspec_adamw_step", _lib.ptr(self.flat), _lib.ptr(self.master),
+                          _lib.ptr(self.exp_avg), _lib.ptr(self.exp_avg_sq), _lib.ptr(self.grads),
+                          self.flat.numel(), *args)
         self.last_step += 1
+        for p in self.params:  # as the reference's step does: the gradients are consumed
+            p.grad = None
         return self.grad_norm()
 
     def grad_norm(self):

@@ -575,6 +575,22 @@ int aspec_adamw_step(void* params, float* master, float* exp_avg, float* exp_avg
                      float beta2, float eps, float max_grad_norm, void* state, void* workspace,
                      void* stream);
 
+/*
+ * The same step with the gradients where autograd leaves them (one tensor per parameter) instead
+ * of one flat buffer: segment i covers the next seg_numel[i] flat parameters and seg_grads[i] is
+ * its bf16 gradient (device pointer, 16-byte aligned), or NULL for a parameter without a gradient,
+ * which is then left unchanged and adds nothing to the norm (as `optimizer.step()` skips a
+ * parameter whose grad is None, optimizer.py:99-109). Each segment keeps its own step count in
+ * `state` (torch's AdamW counts steps per parameter), so its bias corrections count only the steps
+ * in which it had a gradient. Both arrays are host memory; 1 <= nseg <= 64, and every segment but
+ * the last holds a multiple of 8 elements. When every segment has a gradient, the results are
+ * bitwise equal to aspec_adamw_step over the same gradients gathered into one buffer.
+ */
+int aspec_adamw_step_segments(void* params, float* master, float* exp_avg, float* exp_avg_sq,
+                              const void* const* seg_grads, const int64_t* seg_numel, int nseg,
+                              float lr, float weight_decay, float beta1, float beta2, float eps,
+                              float max_grad_norm, void* state, void* workspace, void* stream);
+
 /* ---- Row packing policy (host only: plain host arrays, no GPU, no stream) ---- */
 
 /*

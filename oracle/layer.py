@@ -14,7 +14,9 @@ see oracle/__init__.py.
                 attention), so a full-size geometry stays affordable on the CPU.
 Pinned by tests/test_oracle_layer.py: constant rows normalise to +-w, finite-difference gradients
 of RMSNorm and SwiGLU, silu's value at 0 and its limits, AdamW's closed-form first step
-(p - lr * g / (|g| + eps) for a fresh state) and its clipping and skip rules; layer_forward by
+(p - lr * g / (|g| + eps) for a fresh state) and its clipping and skip rules, and against
+torch.optim.AdamW (float64, clip_grad_norm_) over parameters that miss gradients in some steps;
+layer_forward by
 zeroed sublayers, single-key routing, gate/up order and a hand-computed residual case;
 layer_forward_rows by equality with layer_forward's rows, values and parameter gradients.
 """
@@ -71,16 +73,23 @@ def swiglu_grad(gu, dout):
     return np.concatenate([dout * u * s * (1.0 + g * (1.0 - s)), dout * g * s], axis=-1)
 
 
-def adamw_steps(p, grads, *, lrs, weight_decay=0.0, betas=(0.9, 0.999), eps=1e-8, max_grad_norm=0.5):
+def adamw_steps(p, grads, *, lrs, weight_decay=0.0, betas=(0.9, 0.999), eps=1e-8, max_grad_norm=0.5,
+                active=None):
     """Runs BF16Optimizer steps on a flat fp64 parameter vector for a list of gradients (one per
-    step) and learning rates; returns (params after each step, norms, steps taken)."""
+    step) and learning rates; returns (params after each step, norms, steps taken).
+    `active` (optional, one boolean vector per step) marks the elements whose parameter has a
+    gradient in that step (optimizer.py:99-109): the others add nothing to the norm and are left
+    unchanged, and each element counts its own steps for the bias corrections (torch's AdamW keeps
+    a step count per parameter)."""
     p = np.asarray(p, np.float64).copy()
     m = np.zeros_like(p)
     v = np.zeros_like(p)
+    te = np.zeros(p.shape, np.int64)  # steps in which the element had a gradient
     t = 0
     out, norms = [], []
-    for g, lr in zip(grads, lrs):
-        g = np.asarray(g, np.float64)
+    for k, (g, lr) in enumerate(zip(grads, lrs)):
+        on = np.ones(p.shape, bool) if active is None else np.asarray(active[k], bool)
+        g = np.where(on, np.asarray(g, np.float64), 0.0)
         norm = math.sqrt(float((g * g).sum()))
         norms.append(norm)
         if not math.isfinite(norm):
@@ -89,12 +98,17 @@ def adamw_steps(p, grads, *, lrs, weight_decay=0.0, betas=(0.9, 0.999), eps=1e-8
         coef = min(max_grad_norm / (norm + 1e-6), 1.0) if max_grad_norm > 0 else 1.0
         g = g * coef
         t += 1
-        p = p * (1.0 - lr * weight_decay)
-        m = m + (1.0 - betas[0]) * (g - m)
-        v = betas[1] * v + (1.0 - betas[1]) * g * g
-        bc1 = 1.0 - betas[0] ** t
-        bc2 = 1.0 - betas[1] ** t
-        p = p - (lr / bc1) * m / (np.sqrt(v) / math.sqrt(bc2) + eps)
+        te = te + on
+        bc1 = 1.0 - betas[0] ** te
+        bc2 = 1.0 - betas[1] ** te
+        p_new = p * (1.0 - lr * weight_decay)
+        m_new = m + (1.0 - betas[0]) * (g - m)
+        v_new = betas[1] * v + (1.0 - betas[1]) * g * g
+        with np.errstate(divide="ignore", invalid="ignore"):
+            p_new = p_new - (lr / bc1) * m_new / (np.sqrt(v_new) / np.sqrt(bc2) + eps)
+        p = np.where(on, p_new, p)
+        m = np.where(on, m_new, m)
+        v = np.where(on, v_new, v)
         out.append(p.copy())
     return out, norms, t
 

@@ -77,26 +77,39 @@ class _Params(torch.nn.Module):
         self.frozen = torch.nn.Parameter(torch.randn(9, device=gpu).to(torch.bfloat16), requires_grad=False)
 
 
-def test_fused_adamw_matches_oracle_with_clip_and_skip(gpu):
+def test_fused_adamw_matches_oracle_with_clip_skip_and_missing_gradients(gpu):
+    """Five steps: gradients accumulated in place into the flat buffer (zero_grad(set_to_none=False))
+    or left where autograd puts them (the default), a non-finite step (skipped), a clipped step, and
+    a step in which `b` has no gradient (b untouched, and its bias corrections count its own
+    steps)."""
     mod = _Params(gpu)
     opt = FusedBF16Optimizer(mod, lr=1e-2, weight_decay=0.1, max_grad_norm=5.0, total_steps=10,
                              warmup_ratio=0.2)
     p0 = _np(torch.cat([mod.a.detach().reshape(-1), mod.b.detach().reshape(-1)]).float())
+    na, nb = mod.a.numel(), mod.b.numel()
     g = torch.Generator(device=gpu).manual_seed(12)
-    grads, lrs = [], []
-    for step in range(4):
-        opt.zero_grad()
+    grads, lrs, actives = [], [], []
+    for step in range(5):
+        in_place = step in (0, 2)
+        opt.zero_grad(set_to_none=not in_place)
         ga = torch.randn(mod.a.shape, device=gpu, generator=g) * (0.05 if step != 2 else 3.0)
         gb = torch.randn(mod.b.shape, device=gpu, generator=g) * 0.05
         if step == 1:
             gb[5] = float("nan")  # a non-finite step: skipped
         (mod.a * ga.to(torch.bfloat16)).sum().backward()
-        (mod.b * gb.to(torch.bfloat16)).sum().backward()
-        assert mod.a.grad.data_ptr() == opt.grads.data_ptr()  # accumulated in place
-        grads.append(_np(torch.cat([mod.a.grad.reshape(-1), mod.b.grad.reshape(-1)])))
+        b_has_grad = step != 3
+        if b_has_grad:
+            (mod.b * gb.to(torch.bfloat16)).sum().backward()
+        assert (mod.a.grad.data_ptr() == opt.grads.data_ptr()) == in_place  # accumulated in place
+        grads.append(_np(torch.cat([mod.a.grad.reshape(-1),
+                                    mod.b.grad.reshape(-1) if b_has_grad else torch.zeros_like(mod.b).reshape(-1)])))
+        actives.append(np.concatenate([np.ones(na, bool), np.full(nb, b_has_grad)]))
         lrs.append(opt.get_learning_rate())
+        b_before = _np(mod.b).copy()
         norm = opt.step()
-        want_p, want_norms, want_t = ol.adamw_steps(p0, grads, lrs=lrs, weight_decay=0.1, max_grad_norm=5.0)
+        assert mod.a.grad is None and mod.b.grad is None  # consumed, as the reference's step does
+        want_p, want_norms, want_t = ol.adamw_steps(p0, grads, lrs=lrs, weight_decay=0.1, max_grad_norm=5.0,
+                                                    active=actives)
         got = _np(opt.master[: p0.size])
         print(f"step {step}: lr={lrs[-1]:.3e} norm={float(norm):.4f} oracle={want_norms[-1]:.4f}")
         if np.isfinite(want_norms[-1]):
@@ -104,9 +117,62 @@ def test_fused_adamw_matches_oracle_with_clip_and_skip(gpu):
         else:
             assert not np.isfinite(float(norm))
         np.testing.assert_allclose(got, want_p[-1], rtol=1e-5, atol=1e-6)
-        np.testing.assert_array_equal(_np(mod.a).reshape(-1), _np(opt.master[: mod.a.numel()].to(torch.bfloat16)))
-    assert opt.optimizer_steps() == 3
-    assert lrs == [warmup_decay_lr(i, max_lr=1e-2, total_steps=10, warmup_steps=2) for i in range(4)]
+        np.testing.assert_array_equal(_np(mod.a).reshape(-1), _np(opt.master[:na].to(torch.bfloat16)))
+        if not b_has_grad:
+            np.testing.assert_array_equal(_np(mod.b), b_before)
+    assert opt.optimizer_steps() == 4
+    assert lrs == [warmup_decay_lr(i, max_lr=1e-2, total_steps=10, warmup_steps=2) for i in range(5)]
+
+
+def test_adamw_segments_match_the_flat_step_bit_for_bit(gpu):
+    """aspec_adamw_step_segments over three gradient tensors (the last of odd size) against
+    aspec_adamw_step over the same gradients gathered into one buffer, through the C ABI: master
+    weights, moments, bf16 parameters and the norm are bitwise equal after each of three steps
+    (the second one non-finite, hence skipped)."""
+    import ctypes
+
+    from aspec_amd import _lib
+
+    lib = _lib.load()
+    sizes = [8000, 296, 5]
+    n = sum(sizes)
+    g = torch.Generator(device=gpu).manual_seed(21)
+    p0 = torch.randn(n, device=gpu, generator=g).to(torch.bfloat16)
+    size = ctypes.c_size_t()
+    _lib.call("aspec_adamw_workspace_bytes", ctypes.byref(size))
+
+    def fresh():
+        return {"flat": p0.clone(), "master": p0.float(), "m": torch.zeros(n, device=gpu),
+                "v": torch.zeros(n, device=gpu),
+                "state": torch.zeros(lib.aspec_adamw_state_bytes(), dtype=torch.uint8, device=gpu),
+                "ws": torch.empty(size.value, dtype=torch.uint8, device=gpu)}
+
+    seg, flat = fresh(), fresh()
+    numel = (ctypes.c_int64 * 3)(*sizes)
+    stream = _lib.stream_handle(torch.device(gpu))
+    for step in range(3):
+        parts = [torch.randn(k, device=gpu, generator=g).to(torch.bfloat16) for k in sizes]
+        if step == 1:
+            parts[2][4] = float("inf")
+        gathered = torch.cat(parts)
+        hyper = (1e-2, 0.05, 0.9, 0.999, 1e-8, 1.0)
+        ptrs = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in parts])
+        _lib.call("aspec_adamw_step_segments", _lib.ptr(seg["flat"]), _lib.ptr(seg["master"]),
+                  _lib.ptr(seg["m"]), _lib.ptr(seg["v"]), ptrs, numel, 3, *hyper,
+                  _lib.ptr(seg["state"]), _lib.ptr(seg["ws"]), stream)
+        _lib.call("aspec_adamw_step", _lib.ptr(flat["flat"]), _lib.ptr(flat["master"]),
+                  _lib.ptr(flat["m"]), _lib.ptr(flat["v"]), _lib.ptr(gathered), n, *hyper,
+                  _lib.ptr(flat["state"]), _lib.ptr(flat["ws"]), stream)
+        torch.cuda.synchronize()
+        for key in ("flat", "master", "m", "v"):
+            assert torch.equal(seg[key], flat[key]), (step, key)
+        assert torch.equal(seg["state"][:40], flat["state"][:40]), step
+        assert seg["state"][24:28].view(torch.float32).isfinite().item() == (step != 1)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        bad = (ctypes.c_int64 * 3)(7, 289, 5)
+        _lib.call("aspec_adamw_step_segments", _lib.ptr(seg["flat"]), _lib.ptr(seg["master"]),
+                  _lib.ptr(seg["m"]), _lib.ptr(seg["v"]), ptrs, bad, 3, *hyper,
+                  _lib.ptr(seg["state"]), _lib.ptr(seg["ws"]), stream)
 
 
 def _small_model(gpu, seed=0, draft_vocab=300):
@@ -152,6 +218,14 @@ def test_layer_step_loss_and_gradients_match_oracle(gpu, draft_vocab):
     w = W.from_layout("small", [150, 106], np.array([0, 40, 96, 150, 190]), np.array([0, 0, 0, 1, 1]), 16)
     batch = layer_batch(model, w, seed=6)
     params_before = {n: _np(p) for n, p in model.named_parameters()}
+    seen = {}  # the gradients the optimizer step consumes (it leaves every grad None)
+    step = opt.step
+
+    def keep_and_step(closure=None):
+        seen.update({n: _np(p.grad) for n, p in model.named_parameters() if p.requires_grad})
+        return step(closure)
+
+    opt.step = keep_and_step
     loss, norm = dspark_layer_step(model, opt, batch)
     ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
                        w.block_size, w.sequence_length)
@@ -192,7 +266,7 @@ def test_layer_step_loss_and_gradients_match_oracle(gpu, draft_vocab):
     for n, p in model.named_parameters():
         if p.requires_grad:
             try:
-                _close(f"grad {n}", _np(p.grad), P[n].grad.numpy(), 8e-2, 1.2e-1)
+                _close(f"grad {n}", seen[n], P[n].grad.numpy(), 8e-2, 1.2e-1)
             except AssertionError:
                 bad.append(n)
     assert not bad, bad

@@ -91,6 +91,40 @@ def test_adamw_first_step_closed_form_and_clip():
     assert t2 == 1
 
 
+def test_adamw_oracle_matches_torch_adamw_with_missing_gradients():
+    """Per-parameter activity: a parameter whose grad is None is skipped by torch's AdamW (no decay,
+    no moment update) and keeps its own step count for the bias corrections; the clip norm covers
+    the parameters that have gradients."""
+    r = _rng(3)
+    sizes = [5, 3, 4]
+    p0 = [r.standard_normal(n) for n in sizes]
+    tp = [torch.tensor(x, requires_grad=True) for x in p0]
+    opt = torch.optim.AdamW(tp, lr=1e-2, weight_decay=0.1, foreach=False)
+    has = [[True, True, True], [True, False, True], [False, True, True], [True, True, False],
+           [False, False, True]]
+    grads, actives, lrs = [], [], []
+    for k, on in enumerate(has):
+        gs = [r.standard_normal(n) * 0.4 for n in sizes]
+        for x, g, h in zip(tp, gs, on):
+            x.grad = torch.tensor(g) if h else None
+        torch.nn.utils.clip_grad_norm_([x for x in tp if x.grad is not None], 1.0)
+        lr = 1e-2 * (k + 1)
+        opt.param_groups[0]["lr"] = lr
+        opt.step()
+        grads.append(np.concatenate(gs))
+        actives.append(np.concatenate([np.full(n, h) for n, h in zip(sizes, on)]))
+        lrs.append(lr)
+    out, _, t = ol.adamw_steps(np.concatenate(p0), grads, lrs=lrs, weight_decay=0.1,
+                               max_grad_norm=1.0, active=actives)
+    np.testing.assert_allclose(out[-1], np.concatenate([x.detach().numpy() for x in tp]),
+                               rtol=1e-12, atol=1e-14)
+    assert t == len(has)
+    # a parameter that never had a gradient is untouched
+    out2, _, _ = ol.adamw_steps(np.concatenate(p0), grads[:1], lrs=lrs[:1], weight_decay=0.1,
+                                active=[np.concatenate([np.zeros(5, bool), np.ones(7, bool)])])
+    np.testing.assert_array_equal(out2[0][:5], p0[0])
+
+
 def test_layer_forward_is_differentiable_and_row_local():
     """The oracle layer runs in fp64 with autograd; a draft query whose only visible keys are its
     own block does not see the context."""
