@@ -655,7 +655,8 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
 // dK / dV: key-major. A workgroup owns one 128-key tile and walks one chunk of the (descending)
 // list of query tiles that see it; inside each query tile it visits all G heads of the KV group,
 // so dK/dV are reduced over the GQA group in registers. A key tile covered by one unit is written
-// directly; one split over several units is accumulated in fp32 and finalized.
+// directly; one split over several units writes each unit's fp32 partial to its own slot, and the
+// finalize sums the slots in unit order.
 //
 // Eight waves in two roles share each 32-key slice w = wave % 4:
 //   P waves (0-3):  S = Q K^T (K slice in registers), P = exp2(S*scale*log2e - LSE2) masked,
@@ -667,9 +668,10 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
 // (the P wave's dV product; the dS wave's dS and dK), then starts stage i (S and P; dP), so that
 // a trip begins with MFMAs instead of every wave waiting on the same burst of LDS reads, and the
 // two waves of a SIMD start with complementary work (MFMAs / VALU). Q/dO rows and the row scalars
-// cycle through four LDS stages: stage i is read during trip i only, stage i+1 is landing and
-// stage i+2 is being loaded, straight from global memory into LDS (global_load_lds_dwordx4: no
-// staging registers), so every load has two iterations to arrive. One barrier per iteration.
+// cycle through four LDS stages, straight from global memory into LDS (global_load_lds_dwordx4:
+// no staging registers): stage i is read during trip i only; the dS waves load Q rows and row
+// scalars into stage i+2 at the start of trip i, the P waves load dO rows into stage i+3 at the
+// end of theirs. One barrier per trip.
 // ---------------------------------------------------------------------------------------------
 template <bool P>
 struct Role {
