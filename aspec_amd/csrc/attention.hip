@@ -527,17 +527,31 @@ __global__ void __launch_bounds__(256) attn_bwd_acc_kernel(AttnArgs a) {
   const int chunks = a.plan.b_chunks[n];
   if (chunks <= 1) return;
   const int64_t slot = a.nk * a.hkv * kHeadDim;
+  // Every slot of an element is requested before the first add (the slot count is at most
+  // kMaxChunks), and four elements per thread are in flight at once; the sum still runs over the
+  // slots in unit order.
+#pragma unroll 4
   for (int i = threadIdx.x; i < kBwdTileN * (kHeadDim / 4); i += blockDim.x) {
     const int64_t key = n * kBwdTileN + i / (kHeadDim / 4);
     const int d = (i % (kHeadDim / 4)) * 4;
     if (key >= a.nk) continue;
     const float* pk = a.ws_dk + (key * a.hkv + hkv) * kHeadDim + d;
     const float* pv = a.ws_dv + (key * a.hkv + hkv) * kHeadDim + d;
-    f32x4 k4 = *reinterpret_cast<const f32x4*>(pk);
-    f32x4 v4 = *reinterpret_cast<const f32x4*>(pv);
-    for (int c = 1; c < chunks; ++c) {
-      k4 += *reinterpret_cast<const f32x4*>(pk + c * slot);
-      v4 += *reinterpret_cast<const f32x4*>(pv + c * slot);
+    f32x4 kc[kMaxChunks], vc[kMaxChunks];
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+      if (c < chunks) {
+        kc[c] = *reinterpret_cast<const f32x4*>(pk + c * slot);
+        vc[c] = *reinterpret_cast<const f32x4*>(pv + c * slot);
+      }
+    }
+    f32x4 k4 = kc[0], v4 = vc[0];
+#pragma unroll
+    for (int c = 1; c < kMaxChunks; ++c) {
+      if (c < chunks) {
+        k4 += kc[c];
+        v4 += vc[c];
+      }
     }
     u32x2 wk, wv;
     wk.x = pack_bf16x2(k4[0] * a.scale, k4[1] * a.scale);
