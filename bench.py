@@ -769,7 +769,7 @@ def main():
     teacher_rows = unique_teacher_rows(x)
     pairs, work = kernel_work(w, device, teacher_rows)
     # the loss bytes as the per-row accounting states them (every row reads a full teacher row)
-    survey_bytes = {"loss_fwd": 2 * w.num_queries * VOCAB * 2, "loss_bwd": 3 * w.num_queries * VOCAB * 2,
+    per_row_bytes = {"loss_fwd": 2 * w.num_queries * VOCAB * 2, "loss_bwd": 3 * w.num_queries * VOCAB * 2,
                     "loss_fused": 3 * w.num_queries * VOCAB * 2}
     per_kernel = {}
     for name, stats in kernels.items():
@@ -781,9 +781,9 @@ def main():
         elif bound == "hbm":
             gbs = amount / (stats["mean_ms"] * 1e-3) / 1e9
             entry.update(gbs=round(gbs, 1), frac_hbm=round(gbs / PEAK_HBM_GBS, 4), bytes=amount)
-            if name in survey_bytes:
-                sgbs = survey_bytes[name] / (stats["mean_ms"] * 1e-3) / 1e9
-                entry.update(teacher_rows=teacher_rows, per_row_bytes=survey_bytes[name],
+            if name in per_row_bytes:
+                sgbs = per_row_bytes[name] / (stats["mean_ms"] * 1e-3) / 1e9
+                entry.update(teacher_rows=teacher_rows, per_row_bytes=per_row_bytes[name],
                              per_row_frac_hbm=round(sgbs / PEAK_HBM_GBS, 4))
         per_kernel[name] = entry
     if not args.no_kernel_timing:

@@ -104,7 +104,7 @@ def test_ordered_lists_roundtrip_and_known_answer():
 
 
 def test_config_pair_counts_match_flop_accounting():
-    # Visible pairs per head (SURVEY 8(d) figures, reproduced by the seeded builders).
+    # Visible pairs per head of the benchmark configurations, reproduced by the seeded builders.
     assert M.visible_pairs(_case(W.config1(0))[2]) == 239360
     assert M.visible_pairs(_case(W.config2())[2]) == 16842752
     assert M.visible_pairs(_case(W.config4())[2]) == 537133056
