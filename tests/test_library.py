@@ -46,6 +46,24 @@ def test_size_queries_and_error_codes_without_gpu():
     with pytest.raises(ValueError, match="divisible"):
         _lib.check(lib.aspec_dspark_attn_fwd(None, 0, 0, None, 0, 0, None, 0, 0, None, None,
                                              16, 48, 5, 2, 128, 0.1, None, 0, 0, None, None))
+    # the segmented AdamW validates its host table before any launch
+    assert lib.aspec_adamw_state_bytes() == 40 + 16 * 64  # step, coef, skip, norm + per-segment counts
+
+    def adamw_segments(grads, numel):
+        fake = ctypes.c_void_p(4096)  # never dereferenced: every case below fails validation
+        ptrs = (ctypes.c_void_p * len(grads))(*grads)
+        sizes = (ctypes.c_int64 * len(numel))(*numel)
+        return lib.aspec_adamw_step_segments(fake, fake, fake, fake, ptrs, sizes, len(numel),
+                                             1e-3, 0.0, 0.9, 0.999, 1e-8, 1.0, fake, fake, None)
+
+    with pytest.raises(ValueError, match="multiple of 8"):
+        _lib.check(adamw_segments([4096, 8192], [12, 8]))
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        _lib.check(adamw_segments([4096, 8200], [16, 8]))
+    with pytest.raises(ValueError, match="no elements"):
+        _lib.check(adamw_segments([4096, 0], [16, 0]))
+    with pytest.raises(NotImplementedError, match="segment count"):
+        _lib.check(adamw_segments([4096] * 65, [8] * 65))
 
 
 def test_python_surface_fails_closed_on_cpu():
