@@ -13,7 +13,8 @@ tuning off and this file loaded, later processes reuse the choice. The file carr
 (PyTorch, HIP, hipBLASLt, rocBLAS versions and the GPU arch); on a mismatch TunableOp ignores it
 and the library defaults run.
 
-    python -m aspec_amd.tuning.tune_head_gemms [--out PATH] [--layer-step]
+    python -m aspec_amd.tuning.tune_head_gemms [--out PATH] [--layer-step] [--duration-ms N]
+        [--iterations N] [--rotating-mb MB]
 """
 
 from __future__ import annotations
@@ -32,6 +33,10 @@ def main() -> None:
     p.add_argument("--hidden", type=int, default=4096)
     p.add_argument("--vocab", type=int, default=32000)
     p.add_argument("--layer-step", action="store_true", help="also tune the config-5 layer step's GEMMs")
+    p.add_argument("--duration-ms", type=int, default=30, help="timing budget per candidate solution")
+    p.add_argument("--iterations", type=int, default=30, help="timed runs per candidate solution")
+    p.add_argument("--rotating-mb", type=int, default=0,
+                   help="rotate the operands through this many MB so candidates are timed on cold caches")
     args = p.parse_args()
     import torch
 
@@ -41,8 +46,10 @@ def main() -> None:
     torch.cuda.tunable.enable(True)
     torch.cuda.tunable.tuning_enable(True)
     torch.cuda.tunable.set_filename(str(out))
-    torch.cuda.tunable.set_max_tuning_duration(30)
-    torch.cuda.tunable.set_max_tuning_iterations(30)
+    torch.cuda.tunable.set_max_tuning_duration(args.duration_ms)
+    torch.cuda.tunable.set_max_tuning_iterations(args.iterations)
+    if args.rotating_mb:
+        torch.cuda.tunable.set_rotating_buffer_size(args.rotating_mb)
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(0)
     h = torch.randn(args.rows, args.hidden, device=dev, dtype=torch.bfloat16, generator=g)
