@@ -49,8 +49,6 @@ class _SelectiveHeadObjective(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_objective, *unused):
-        if ctx.check is not None:
-            ctx.check.raise_if_bad()
         dlogits, weight_t = ctx.saved_tensors
         with _timing.region("head_gemm_dgrad"):
             dh = torch.matmul(dlogits, weight_t.t())
@@ -59,6 +57,11 @@ class _SelectiveHeadObjective(torch.autograd.Function):
             g = grad_objective.detach().reshape(()).to(device=dh.device, dtype=torch.float32)
             _lib.call("aspec_scale_bf16_by_device_scalar", dh.data_ptr(), dh.numel(), g.data_ptr(),
                       _lib.stream_handle(dh.device))
+        # The forward's index flag is read only now, with the dgrad GEMM already queued behind the
+        # loss pass: the host waits for the loss kernel while the GPU has the GEMM to run, and a bad
+        # index still raises before dh reaches the caller.
+        if ctx.check is not None:
+            ctx.check.raise_if_bad()
         return dh, None, None, None, None, None, None, None, None, None, None
 
 

@@ -23,8 +23,9 @@ class IndexCheck:
 
     The forward ORs bit 1 (teacher index) / bit 2 (target) into a device flag and writes NaN rows.
     The flag is copied into pinned host memory behind an event on the launch stream, so reading it
-    later costs no stall: the backward reads it before it launches, and a forward that no backward
-    will follow reads it at once. Either raises ValueError."""
+    later costs no stall: the backward reads it after its own kernels are queued (the GPU keeps
+    working while the host waits for the forward's flag), and a forward that no backward will
+    follow reads it at once. Either raises ValueError before a result reaches the caller."""
 
     def __init__(self, flags: torch.Tensor):
         self.host = torch.empty(1, dtype=torch.int32, pin_memory=True)
@@ -103,8 +104,6 @@ class _CeL1(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_ce, grad_l1, grad_argmax=None):
-        if ctx.index_check is not None:
-            ctx.index_check.raise_if_bad()
         logits, targets, teacher, indices, stats = ctx.saved_tensors
         vocab = logits.shape[-1]
         rows = logits.numel() // vocab
@@ -112,12 +111,17 @@ class _CeL1(torch.autograd.Function):
         gl1 = None if (grad_l1 is None or teacher is None) else grad_l1.to(torch.float32).contiguous()
         grad_logits = torch.empty_like(logits)
         if gce is None and gl1 is None:
-            return grad_logits.zero_(), None, None, None, None, None, None
-        with _timing.region("loss_bwd"):
-            _lib.call("aspec_ce_l1_bwd", _lib.ptr(logits), _lib.ptr(teacher), _lib.ptr(indices),
-                      ctx.trows, _lib.ptr(targets), ctx.ignore_index, rows, vocab, _lib.ptr(stats),
-                      _lib.ptr(gl1), _lib.ptr(gce), _lib.ptr(grad_logits),
-                      _lib.stream_handle(logits.device))
+            grad_logits.zero_()
+        else:
+            with _timing.region("loss_bwd"):
+                _lib.call("aspec_ce_l1_bwd", _lib.ptr(logits), _lib.ptr(teacher), _lib.ptr(indices),
+                          ctx.trows, _lib.ptr(targets), ctx.ignore_index, rows, vocab, _lib.ptr(stats),
+                          _lib.ptr(gl1), _lib.ptr(gce), _lib.ptr(grad_logits),
+                          _lib.stream_handle(logits.device))
+        # the forward's index flag, read after this backward's launch is queued (no GPU idle time);
+        # a bad index raises before the gradient reaches the caller
+        if ctx.index_check is not None:
+            ctx.index_check.raise_if_bad()
         return grad_logits, None, None, None, None, None, None
 
 

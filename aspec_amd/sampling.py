@@ -124,8 +124,6 @@ class _SampledL1(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_l1):
-        if ctx.check is not None:
-            ctx.check.raise_if_bad()
         flat, table, indices, stats = ctx.saved_tensors
         rows, vocab = flat.shape
         g = grad_l1.reshape(rows).to(torch.float32).contiguous()
@@ -134,6 +132,9 @@ class _SampledL1(torch.autograd.Function):
             _lib.call("aspec_sampled_l1_bwd", flat.data_ptr(), table.data_ptr(), _lib.ptr(indices),
                       table.shape[0], rows, vocab, stats.data_ptr(), g.data_ptr(), dx.data_ptr(),
                       _lib.stream_handle(flat.device))
+        # the forward's index flag, read with this backward's kernel already queued
+        if ctx.check is not None:
+            ctx.check.raise_if_bad()
         return dx.view(ctx.shape), None, None, None, None
 
 

@@ -55,9 +55,6 @@ class _TiledL1(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, gradient):
-        check = getattr(ctx, "index_check", None)
-        if check is not None:
-            check.raise_if_bad()
         logits, target, stats, indices = ctx.saved_tensors
         vocab = logits.shape[-1]
         rows = logits.numel() // vocab
@@ -67,6 +64,10 @@ class _TiledL1(torch.autograd.Function):
                   target.shape[0] if indices is not None else rows, None, -100, rows, vocab,
                   _lib.ptr(stats), _lib.ptr(g), None, _lib.ptr(grad_logits),
                   _lib.stream_handle(logits.device))
+        # the forward's index flag, read with this backward's kernel already queued
+        check = getattr(ctx, "index_check", None)
+        if check is not None:
+            check.raise_if_bad()
         return grad_logits, None, None, None
 
 

@@ -12,13 +12,20 @@ All layouts are deterministic given the seed; nothing here reads data from disk.
   config 4: one 32768-token document, 2048 anchors at linspace(0, 32768 - 16, 2048), GQA 40/8.
   config 5: 3 documents of seeded lengths (sum 4096), an anchor every 8 doc-local tokens
             (u <= L - B - 1), B = 16, GQA 32/8 x 128: the full one-layer training step's row.
+  reference_b7: the reference's published attention study (10 x 4096 + 40960 + 49152 context
+            tokens, 512 captured anchors per document, B = 7, GQA 32/8 x 128), read from
+            tests/golden/dspark_b7_workload.json.
 """
 
 from __future__ import annotations
 
+import json
 from dataclasses import dataclass
+from pathlib import Path
 
 import numpy as np
+
+B7_FIXTURE = Path(__file__).resolve().parent.parent / "tests" / "golden" / "dspark_b7_workload.json"
 
 
 @dataclass
@@ -131,6 +138,32 @@ def config5(seed: int = 0) -> Workload:
     starts = np.concatenate([[0], np.cumsum(lengths)[:-1]])
     anchors = anchors - np.concatenate([[0], np.cumsum(np.asarray(lengths) - 1)[:-1]])[docs] + starts[docs]
     return from_layout("config5", lengths, anchors, docs, 16)
+
+
+def reference_b7(path=None) -> Workload:
+    """The workload of the reference's DSpark B=7 attention study
+    (tools/performance/bench_dspark_b7_attention.py; docs/dspark_attn_kernel_optimization.md:49-51):
+    twelve documents packed into one 131072-token row, each with its 512 captured document-local
+    anchors in the sampler's order, B = 7, so 43008 draft queries and 174080 keys. Per document
+    the visible keys are its prefix before the anchor plus the anchor's own block, exactly the
+    reference's per-document THD segments laid end to end."""
+    data = json.loads(Path(path or B7_FIXTURE).read_text())
+    lengths = [int(n) for n in data["lengths"]]
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int64)
+    anchors, docs = [], []
+    for d, local in enumerate(data["anchor_positions"]):
+        anchors.append(starts[d] + np.asarray(local, np.int64))
+        docs.append(np.full(len(local), d, np.int64))
+    return from_layout("reference_b7", lengths, np.concatenate(anchors), np.concatenate(docs),
+                       int(data["block"]))
+
+
+def reference_b7_published(path=None) -> dict:
+    """The study's own figures (SM100): per route, median/min/max ms of fwd, bwd and fb, and its
+    timing contract."""
+    data = json.loads(Path(path or B7_FIXTURE).read_text())
+    return {"architecture": data["architecture"], "timing_contract": data["timing_contract"],
+            "ms": data["published_ms"]}
 
 
 def reference_test_layout(block_size: int, lengths=(257, 263, 19), drop_doc: bool = True) -> Workload:

@@ -331,3 +331,68 @@ def test_direct_cp_packed_batch_of_two_cudnn_backend(gpu):
             torch.testing.assert_close(got.float().cpu(), ref, atol=0.06, rtol=0.08)
     with pytest.raises(ValueError, match="one controller-owned row"):
         direct_cp_attention(*[x.detach() for x in dev], DirectCPMetadata(**common, backend="fa4"))
+
+
+def _grads_fresh(fn, inputs, dout):
+    out = fn(*inputs)
+    return torch.autograd.grad(out, inputs, dout)
+
+
+def test_cudnn_flex_attention_multiple_live_autograd_graphs(gpu):
+    """Two pending graphs over one mask, consumed in reverse order (the reference's
+    tests/test_cudnn_internal_gqa_gpu.py:93-123): each call owns its scratch, so each graph's
+    gradients equal a fresh forward + backward of the same inputs bit for bit (the HIP backward
+    is deterministic), for both GQA modes."""
+    torch.manual_seed(330)
+    qshape, kshape = (1, 71, 8, 128), (1, 229, 2, 128)
+    ends = torch.full((71,), 229, device=gpu, dtype=torch.int32)
+    zeros = torch.zeros_like(ends)
+    mask = CudnnFlexMask(torch.stack((zeros, zeros, ends, ends, ends))[None])
+    for mode in ("internal", "native"):
+        inputs = [[torch.randn(shape, device=gpu, dtype=torch.bfloat16).requires_grad_()
+                   for shape in (qshape, kshape, kshape)] for _ in range(2)]
+        dout = [torch.randn(qshape, device=gpu, dtype=torch.bfloat16) for _ in inputs]
+        fn = lambda q, k, v: cudnn_flex_attention(q, k, v, mask=mask, scale=128 ** -0.5, gqa_mode=mode)  # noqa: E731
+        outputs = [fn(*values) for values in inputs]
+        actual = [None, None]
+        for index in (1, 0):
+            actual[index] = torch.autograd.grad(outputs[index], inputs[index], dout[index])
+        for values, grads, d in zip(inputs, actual, dout):
+            expected = _grads_fresh(fn, values, d)
+            for got, ref in zip(grads, expected):
+                assert torch.equal(got, ref)
+                assert torch.isfinite(got).all()
+
+
+def test_direct_cp_multiple_live_autograd_graphs(gpu):
+    """The same for `direct_cp_attention_from_kv`: two pending graphs sharing one metadata object
+    (and so one cached plan), consumed in reverse order, each equal bit for bit to a fresh
+    forward + backward, and the first also within the reference's bars of the oracle."""
+    w = W.config1(0)
+    w.q_heads, w.kv_heads = 8, 2
+    meta = W.metadata_for(w, gpu)
+    g = torch.Generator(device=gpu).manual_seed(331)
+
+    def rows(n, h):
+        return torch.randn(1, n, h, w.head_dim, device=gpu, generator=g).to(torch.bfloat16).transpose(1, 2)
+
+    inputs = [[rows(w.num_queries, 8).requires_grad_(), rows(w.num_keys, 2).requires_grad_(),
+               rows(w.num_keys, 2).requires_grad_()] for _ in range(2)]
+    dout = [rows(w.num_queries, 8) for _ in inputs]
+    fn = lambda q, k, v: direct_cp_attention_from_kv(q, k, v, meta)[0]  # noqa: E731
+    outputs = [fn(*values) for values in inputs]
+    actual = [None, None]
+    for index in (1, 0):
+        actual[index] = torch.autograd.grad(outputs[index], inputs[index], dout[index])
+    for values, grads, d in zip(inputs, actual, dout):
+        expected = _grads_fresh(fn, values, d)
+        for got, ref in zip(grads, expected):
+            assert torch.equal(got, ref)
+    ends = M.endpoints(w.anchors, w.keep, w.anchor_doc_ids, w.context_positions, w.ctx_doc_ids,
+                       w.block_size, w.sequence_length)
+    vis = M.endpoints_to_dense(ends, w.num_keys)
+    q, k, v = (x.detach()[0].float().cpu() for x in inputs[0])
+    _, _, ref = A.attention(q, k, v, vis, w.head_dim ** -0.5, dout=dout[0][0].float().cpu(),
+                            dtype=torch.float32)
+    for got, r in zip(actual[0], ref):
+        torch.testing.assert_close(got[0].float().cpu(), r, atol=0.04, rtol=0.04)

@@ -33,6 +33,38 @@ def test_tiled_l1_matches_fp64_oracle_and_bf16_gradient(gpu, vocab, scale):
     torch.testing.assert_close(grad.cpu(), ref_grad.to(torch.bfloat16), atol=1e-7, rtol=0.02)
 
 
+def test_tiled_l1_offsets_beyond_signed_int32_match_last_row_oracle(gpu):
+    """The reference's >2^31-element pointer-offset regression (tests/test_tiled_l1.py:59-85): at
+    V = 151936 (the streaming kernel) 14136 zero rows plus a random last row, so the last row
+    starts past element 2^31 of both the logits and dlogits; its loss and gradient match the fp64
+    oracle and the zero rows stay exactly zero (about 13 GB of device memory)."""
+    if torch.cuda.mem_get_info()[0] < 16 * 1024**3:
+        pytest.skip("large-offset regression needs 16 GiB of free device memory")
+    vocab = 151936
+    rows = (2**31) // vocab + 2
+    assert (rows - 1) * vocab > 2**31
+    draft = torch.zeros(rows, vocab, device=gpu, dtype=torch.bfloat16)
+    teacher = torch.zeros_like(draft)
+    g = torch.Generator(device=gpu).manual_seed(872)
+    last = torch.randn(vocab, device=gpu, dtype=torch.bfloat16, generator=g)
+    last_teacher = torch.randn(vocab, device=gpu, dtype=torch.bfloat16, generator=g)
+    draft[-1].copy_(last)
+    teacher[-1].copy_(last_teacher)
+    draft.requires_grad_()
+    loss = tiled_l1_from_logits(draft, teacher)
+    loss.sum().backward()
+    torch.cuda.synchronize()
+    xd, yd = last.double().cpu().numpy()[None], last_teacher.double().cpu().numpy()[None]
+    np.testing.assert_allclose(loss[-1:].detach().double().cpu().numpy(), L.l1(xd, yd), atol=2e-6, rtol=2e-6)
+    ref_grad = torch.as_tensor(L.l1_grad(xd, yd, np.ones(1)))[0]
+    torch.testing.assert_close(draft.grad[-1].cpu(), ref_grad.to(torch.bfloat16), atol=1e-7, rtol=0.02)
+    assert loss[0].item() == 0
+    assert not draft.grad[0].count_nonzero()
+    assert not draft.grad[rows // 2].count_nonzero()
+    del draft, teacher, loss
+    torch.cuda.empty_cache()
+
+
 def test_identical_distributions_have_zero_loss_and_gradient(gpu):
     for vocab in (4103, 32000):
         draft = torch.randn(5, vocab, device=gpu, dtype=torch.bfloat16, requires_grad=True)

@@ -11,8 +11,14 @@ oracle on CPU. Tolerances are the reference's bf16-GPU-vs-math bars
 Loss at config 2's shape (8192 rows x V = 32000, a 4096-row teacher table addressed by the DSpark
 teacher indices, CE targets from the DSpark labels): CE and L1 of every row against the fp64 oracle
 (the reference's bars, tests/test_tiled_l1.py:28-46: L1 atol = rtol = 2e-6; CE 2e-5 / 2e-6) and the
-gradient of 96 sampled rows spread over the persistent kernel's row walk (rel-L2 < 0.01,
-atol 1e-6 / rtol 0.02 in bf16, the bar of the fused CE + L1 gradient test).
+gradient of >= 96 sampled rows spread over the persistent kernel's row walk (rel-L2 < 0.01,
+atol 1e-6 / rtol 0.02 in bf16, the bar of the fused CE + L1 gradient test), for the two-kernel
+path (forward walk, then the backward kernel) and for the one-pass kernel the draft step runs
+(`ce_l1_fused_grad`: the forward walk writes the objective's dlogits, with the DSpark
+eval-mask x decay weights).
+
+The reference's B = 7 attention study workload (10 x 4096 + 40960 + 49152 context tokens, 6144
+captured anchors; tests/golden/dspark_b7_workload.json): every output of two KV groups.
 
 Each output's max-abs and relative-L2 error is printed and, when ASPEC_PARITY_DIR is set, appended
 as one JSON line to $ASPEC_PARITY_DIR/parity.jsonl.
@@ -122,17 +128,21 @@ def test_config4_attention_one_kv_group_elementwise(gpu):
     _attention_parity(w, gpu, (3,), seed=41, case="config4")
 
 
-def test_config2_loss_all_rows_indexed_teacher(gpu):
-    """CE + L1 at 8192 x 32000 with the DSpark indexed teacher: the bench's persistent forward
-    (one workgroup per CU walking 32 rows each, the next row's teacher index and target prefetched
-    while the current row is reduced) checked on every row, and the fused backward on 96 rows:
-    the first and last rows of the walk and rows at the CU-count strides."""
-    from aspec_amd.loss import ce_l1_from_logits
+def test_reference_b7_workload_two_kv_groups_elementwise(gpu):
+    """The reference's published attention workload (docs/dspark_attn_kernel_optimization.md:49-51):
+    B = 7 blocks straddle the kernels' 32-row query tiles and 64/128-key tiles, twelve documents
+    share one key space, and the anchors are in the sampler's order (one wraparound per
+    document). O, LSE, dQ of all 43008 rows and dK, dV of all 174080 keys for KV groups 0 and 7."""
+    w = W.reference_b7()
+    _attention_parity(w, gpu, (0, w.kv_heads - 1), seed=70, case="reference_b7")
+
+
+def _config2_loss_inputs(gpu, seed):
     from aspec_amd.targets import dspark_targets
 
     w = W.config2()
     vocab, rows = 32000, w.num_queries
-    g = torch.Generator(device=gpu).manual_seed(52)
+    g = torch.Generator(device=gpu).manual_seed(seed)
     anchors = torch.as_tensor(w.anchors, device=gpu)[None]
     keep = torch.as_tensor(w.keep, device=gpu)[None]
     input_ids = torch.randint(0, vocab, (1, w.context_length), device=gpu, generator=g)
@@ -145,12 +155,13 @@ def test_config2_loss_all_rows_indexed_teacher(gpu):
     tidx = tg.teacher_index.reshape(-1).contiguous()
     x = (torch.randn(rows, vocab, device=gpu, generator=g) * 2).bfloat16()
     table = (torch.randn(w.context_length, vocab, device=gpu, generator=g) * 2).bfloat16()
-    gce = torch.randn(rows, device=gpu, generator=g)
-    gl1 = torch.randn(rows, device=gpu, generator=g)
-    xin = x.clone().requires_grad_()
-    ce, l1 = ce_l1_from_logits(xin, targets, table, teacher_indices=tidx)
-    ((ce * gce).sum() + (l1 * gl1).sum()).backward()
-    torch.cuda.synchronize()
+    return w, tg, targets, tidx, x, table
+
+
+def _loss_oracle_check(case, x, table, targets, tidx, ce, l1, dlogits, gce, gl1):
+    """CE and L1 of every row, and dlogits of >= 96 rows spread over the persistent walk, against
+    the fp64 oracle."""
+    rows = x.shape[0]
     xc, tc, ic = x.cpu(), targets.cpu().numpy(), tidx.cpu().numpy()
     table_c = table.cpu()
     ref_ce, ref_l1 = np.empty(rows), np.empty(rows)
@@ -159,17 +170,55 @@ def test_config2_loss_all_rows_indexed_teacher(gpu):
         yd = table_c[torch.as_tensor(ic[r0:r0 + 512])].double().numpy()
         ref_ce[r0:r0 + 512] = L.cross_entropy(xd, tc[r0:r0 + 512])
         ref_l1[r0:r0 + 512] = L.l1(xd, yd)
-    record("config2_loss", "CE", ce.detach().cpu(), torch.as_tensor(ref_ce), atol=2e-5, rtol=2e-6)
-    record("config2_loss", "L1", l1.detach().cpu(), torch.as_tensor(ref_l1), atol=2e-6, rtol=2e-6)
-    sample = np.unique(np.concatenate([np.arange(4), np.arange(rows - 4, rows),
-                                       np.arange(0, rows, 256)[:40] + 1, np.arange(255, rows, 256)[:40],
+    record(case, "CE", ce.detach().cpu(), torch.as_tensor(ref_ce), atol=2e-5, rtol=2e-6)
+    record(case, "L1", l1.detach().cpu(), torch.as_tensor(ref_l1), atol=2e-6, rtol=2e-6)
+    # the walk's first and last rows, rows at the CU-count stride (start, middle and end of each
+    # CU's share) and a few at an odd stride
+    sample = np.unique(np.concatenate([np.arange(4), np.arange(rows - 4, rows), np.arange(1, rows, 256),
+                                       np.arange(128, rows, 256), np.arange(255, rows, 256),
                                        np.arange(1, rows, 97)[:8]]))
+    assert sample.size >= 96
     xd = xc[sample].double().numpy()
     yd = table_c[torch.as_tensor(ic[sample])].double().numpy()
     ref_g = (L.cross_entropy_grad(xd, tc[sample], gce.cpu().double().numpy()[sample])
              + L.l1_grad(xd, yd, gl1.cpu().double().numpy()[sample]))
-    got_g = xin.grad[torch.as_tensor(sample, device=gpu)].cpu()
-    _, rel = record("config2_loss", "dlogits (sampled rows)", got_g.double(), torch.as_tensor(ref_g),
+    got_g = dlogits[torch.as_tensor(sample, device=dlogits.device)].cpu()
+    _, rel = record(case, "dlogits (sampled rows)", got_g.double(), torch.as_tensor(ref_g),
                     atol=1e-6, rtol=0.02)
     assert rel < 0.01
     torch.testing.assert_close(got_g, torch.as_tensor(ref_g).to(torch.bfloat16), atol=1e-6, rtol=0.02)
+
+
+def test_config2_fused_loss_all_rows_indexed_teacher(gpu):
+    """The one-pass loss the draft step ships (`ce_l1_fused_grad`: the persistent forward walk,
+    32 rows per CU at 8192 rows, writing the objective's dlogits as each row's statistics are
+    final) with the DSpark indexed teacher and the step's weights (0.1 / 0.9 times the eval mask x
+    exp(-k/4) decay over their sum): CE and L1 of every row, dlogits of >= 96 rows over the walk."""
+    from aspec_amd.loss import ce_l1_fused_grad
+
+    w, tg, targets, tidx, x, table = _config2_loss_inputs(gpu, 53)
+    wts = tg.weights.reshape(-1).float()
+    gce, gl1 = 0.1 * wts / wts.sum(), 0.9 * wts / wts.sum()
+    ce, l1, dlogits = ce_l1_fused_grad(x, targets, table, ce_weights=gce, l1_weights=gl1,
+                                       teacher_indices=tidx)
+    torch.cuda.synchronize()
+    _loss_oracle_check("config2_fused_loss", x, table, targets, tidx, ce, l1, dlogits, gce, gl1)
+
+
+def test_config2_loss_all_rows_indexed_teacher(gpu):
+    """CE + L1 at 8192 x 32000 with the DSpark indexed teacher: the bench's persistent forward
+    (one workgroup per CU walking 32 rows each, the next row's teacher index and target prefetched
+    while the current row is reduced) checked on every row, and the fused backward on 96 rows:
+    the first and last rows of the walk and rows at the CU-count strides."""
+    from aspec_amd.loss import ce_l1_from_logits
+
+    w, tg, targets, tidx, x, table = _config2_loss_inputs(gpu, 52)
+    rows = x.shape[0]
+    g = torch.Generator(device=gpu).manual_seed(152)
+    gce = torch.randn(rows, device=gpu, generator=g)
+    gl1 = torch.randn(rows, device=gpu, generator=g)
+    xin = x.clone().requires_grad_()
+    ce, l1 = ce_l1_from_logits(xin, targets, table, teacher_indices=tidx)
+    ((ce * gce).sum() + (l1 * gl1).sum()).backward()
+    torch.cuda.synchronize()
+    _loss_oracle_check("config2_loss", x, table, targets, tidx, ce, l1, xin.grad, gce, gl1)
