@@ -28,6 +28,8 @@ from aspec_amd.direct_cp import (  # noqa: F401
     direct_cp_attention,
     direct_cp_attention_from_kv,
     direct_cp_attention_observation,
+    direct_cp_partial_attention,
+    merge_attention_partials,
 )
 from aspec_amd.dspark_head import (  # noqa: F401
     AcceptRatePredictor,
@@ -99,6 +101,8 @@ __all__ = [
     "direct_cp_attention",
     "direct_cp_attention_from_kv",
     "direct_cp_attention_observation",
+    "direct_cp_partial_attention",
+    "merge_attention_partials",
     "thd_fa4_attention",
     "tiled_l1_from_logits",
 ]

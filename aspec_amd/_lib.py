@@ -26,6 +26,8 @@ SIGNATURES = {
     "aspec_last_error": (ctypes.c_char_p, []),
     "aspec_thd_row_metadata": (_int, [_c_void_p] * 5 + [_i64] * 6 + [_int] + [_c_void_p] * 5),
     "aspec_thd_batch_row_metadata": (_int, [_c_void_p] * 5 + [_i64] * 7 + [_int] + [_c_void_p] * 5),
+    "aspec_thd_cp_shard_endpoints": (_int, [_c_void_p] * 5 + [_i64] * 4 + [_c_void_p, _i64, _c_void_p, _i64]
+                                     + [_i64] * 3 + [_int] + [_c_void_p] * 3),
     "aspec_dspark_mla_mask_workspace_bytes": (_int, [_i64, _i64, _size_p]),
     "aspec_dspark_mla_mask": (_int, [_c_void_p] * 3 + [_i64] * 4 + [_int] + [_i64] * 2 + [_c_void_p] * 4),
     "aspec_flex_mask_intervals": (_int, [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _i64, _i64]
@@ -127,7 +129,7 @@ SIGNATURES = {
     "aspec_pack_work_aware_rows": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3),
 }
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _lock = threading.Lock()
 _lib = None

@@ -27,8 +27,6 @@ COMMON_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
-    # fp32 atomicAdd as the hardware global_atomic_add_f32, not a compare-and-swap loop.
-    "-munsafe-fp-atomics",
     # Packed FP32 (v_pk_*_f32) stays off: scalar fp32 code only.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # Run LLVM's machine verifier on the device code: an instruction selected with an operand of

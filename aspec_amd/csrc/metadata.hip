@@ -142,6 +142,104 @@ __global__ void row_metadata_kernel(RowArgs a) {
   }
 }
 
+// One context-parallel rank's partial (direct_cp.py:750-878 with cp_size > 1): every query row of
+// the collective block order against this rank's keys, its context shard (ascending positions)
+// followed by the draft keys of its own blocks. Query block rc is block query_blocks[rc]; its draft
+// keys are those of local slot j when local_blocks[j] is that block (local_blocks ascending), and
+// otherwise absent: both draft endpoints are the key length K_local, as the reference writes them.
+struct ShardArgs {
+  const int64_t* anchors;      // [batch][num_blocks], original block order
+  const uint8_t* keep;
+  const int64_t* anchor_docs;
+  const int64_t* ctx_pos;      // [batch][T] this rank's context positions
+  const int64_t* ctx_docs;
+  const int64_t* query_blocks;  // [nqb] collective order
+  const int64_t* local_blocks;  // [nlb] ascending
+  int64_t num_blocks, nqb, nlb, block, T, seq_len, ctx_window, q_window;
+  int causal;
+  int32_t* ends;  // [5][batch * nqb * block]
+  int32_t* flags;
+};
+
+__global__ void shard_endpoints_kernel(ShardArgs a) {
+  const int64_t nq = a.nqb * a.block;
+  const int64_t K = a.T + a.nlb * a.block;
+  const int64_t b = blockIdx.y;
+  const int64_t NQ = static_cast<int64_t>(gridDim.y) * nq;
+  a.anchors += b * a.num_blocks;
+  a.keep += b * a.num_blocks;
+  a.anchor_docs += b * a.num_blocks;
+  a.ctx_pos += b * a.T;
+  a.ctx_docs += b * a.T;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tid < nq) {
+    const int64_t q = tid;
+    const int64_t rc = q / a.block;
+    const int64_t o = q - rc * a.block;
+    const int64_t r = a.query_blocks[rc];
+    if (r < 0 || r >= a.num_blocks) {
+      atomicOr(a.flags, 4);
+      for (int e = 0; e < 5; ++e) a.ends[e * NQ + b * nq + q] = 0;
+      return;
+    }
+    const int64_t anchor = a.anchors[r];
+    const int64_t doc = a.anchor_docs[r];
+    const bool token_keep = a.keep[r] != 0 && (a.seq_len <= 0 || anchor + o < a.seq_len);
+    const bool query_keep = token_keep && doc >= 0;
+    int64_t cb = 0, ce = 0, db = 0, de = 0;
+    if (query_keep) {
+      int64_t lower = 0;
+      if (a.ctx_window > 0) lower = max(lower, anchor - a.ctx_window);
+      if (a.q_window > 0) lower = max(lower, anchor + o - a.q_window + 1);
+      cb = lower_bound(a.ctx_pos, a.T, lower);
+      ce = lower_bound(a.ctx_pos, a.T, anchor);
+      const int64_t sd = sortable_doc(doc);
+      cb = max(cb, doc_bound(a.ctx_docs, a.T, sd, false));
+      ce = min(ce, doc_bound(a.ctx_docs, a.T, sd, true));
+      cb = min(cb, ce);
+      const int64_t j = lower_bound(a.local_blocks, a.nlb, r);
+      if (j < a.nlb && a.local_blocks[j] == r) {
+        const int64_t base = a.T + j * a.block;
+        int64_t valid = a.block;
+        if (a.seq_len > 0) valid = min(max(a.seq_len - anchor, (int64_t)0), a.block);
+        db = base;
+        de = base + valid;
+        if (a.causal) de = min(de, base + o + 1);
+        if (a.q_window > 0) {
+          db = base + max(o - a.q_window + 1, (int64_t)0);
+          de = min(de, base + min(o + a.q_window, a.block));
+        }
+        db = min(db, de);
+      } else {
+        db = de = K;
+      }
+      const int64_t key0 = b * K;
+      cb += key0;
+      ce += key0;
+      db += key0;
+      de += key0;
+    }
+    a.ends[0 * NQ + b * nq + q] = 0;
+    a.ends[1 * NQ + b * nq + q] = static_cast<int32_t>(cb);
+    a.ends[2 * NQ + b * nq + q] = static_cast<int32_t>(ce);
+    a.ends[3 * NQ + b * nq + q] = static_cast<int32_t>(db);
+    a.ends[4 * NQ + b * nq + q] = static_cast<int32_t>(de);
+  } else if (tid < nq + a.T) {
+    const int64_t t = tid - nq;
+    if (t > 0) {
+      int bad = 0;
+      if (a.ctx_pos[t] < a.ctx_pos[t - 1]) bad |= 1;
+      if (sortable_doc(a.ctx_docs[t]) < sortable_doc(a.ctx_docs[t - 1])) bad |= 2;
+      if (bad) atomicOr(a.flags, bad);
+    }
+  } else if (tid < nq + a.T + a.nlb && b == 0) {
+    const int64_t j = tid - nq - a.T;
+    if (a.local_blocks[j] < 0 || a.local_blocks[j] >= a.num_blocks ||
+        (j > 0 && a.local_blocks[j] <= a.local_blocks[j - 1]))
+      atomicOr(a.flags, 4);
+  }
+}
+
 struct AuxArgs {
   const int32_t* qaux;  // [4][nq]: anchors, keep, blocks, docs
   const int32_t* kaux;  // [4][nk]: docs, positions, blocks, keep
@@ -424,6 +522,66 @@ extern "C" int aspec_thd_batch_row_metadata(const int64_t* anchors, const uint8_
                      dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(batch)),
                      dim3(threads), 0, static_cast<hipStream_t>(stream), a);
   return check_launch("row_metadata_kernel");
+}
+
+extern "C" int aspec_thd_cp_shard_endpoints(const int64_t* anchors, const uint8_t* keep,
+                                            const int64_t* anchor_docs,
+                                            const int64_t* context_positions,
+                                            const int64_t* context_docs, int64_t batch,
+                                            int64_t num_blocks, int64_t block_size,
+                                            int64_t context_length, const int64_t* query_blocks,
+                                            int64_t num_query_blocks, const int64_t* local_blocks,
+                                            int64_t num_local_blocks, int64_t sequence_length,
+                                            int64_t context_window, int64_t query_window,
+                                            int draft_is_causal, int32_t* endpoints,
+                                            int32_t* status_flags, void* stream) {
+  if (batch <= 0 || batch > 65535 || num_blocks < 0 || block_size <= 0 || context_length < 0 ||
+      num_query_blocks < 0 || num_local_blocks < 0 || num_local_blocks > num_blocks)
+    return set_error(ASPEC_ERR_INVALID,
+                     "invalid CP shard geometry (batch=%lld, blocks=%lld, query blocks=%lld, "
+                     "local blocks=%lld, block=%lld, T=%lld)",
+                     (long long)batch, (long long)num_blocks, (long long)num_query_blocks,
+                     (long long)num_local_blocks, (long long)block_size, (long long)context_length);
+  const int64_t nq = num_query_blocks * block_size;
+  const int64_t K = context_length + num_local_blocks * block_size;
+  if (batch * K >= (1LL << 31) - 1 || batch * nq >= (1LL << 31) - 1)
+    return set_error(ASPEC_ERR_INVALID, "CP shard metadata exceeds int32 indexing (%lld keys)",
+                     (long long)(batch * K));
+  if (!endpoints || !status_flags)
+    return set_error(ASPEC_ERR_INVALID, "endpoints and status flags are required");
+  if (num_blocks > 0 && (!anchors || !keep || !anchor_docs))
+    return set_error(ASPEC_ERR_INVALID, "anchors, keep and anchor_docs are required");
+  if ((num_query_blocks > 0 && !query_blocks) || (num_local_blocks > 0 && !local_blocks))
+    return set_error(ASPEC_ERR_INVALID, "query and local block ids are required");
+  if (context_length > 0 && (!context_positions || !context_docs))
+    return set_error(ASPEC_ERR_INVALID, "context positions and document ids are required");
+  const int64_t total = nq + context_length + num_local_blocks;
+  if (total == 0) return ASPEC_OK;
+  ShardArgs a;
+  a.anchors = anchors;
+  a.keep = keep;
+  a.anchor_docs = anchor_docs;
+  a.ctx_pos = context_positions;
+  a.ctx_docs = context_docs;
+  a.query_blocks = query_blocks;
+  a.local_blocks = local_blocks;
+  a.num_blocks = num_blocks;
+  a.nqb = num_query_blocks;
+  a.nlb = num_local_blocks;
+  a.block = block_size;
+  a.T = context_length;
+  a.seq_len = sequence_length;
+  a.ctx_window = context_window;
+  a.q_window = query_window;
+  a.causal = draft_is_causal;
+  a.ends = endpoints;
+  a.flags = status_flags;
+  const int threads = 256;
+  const int64_t blocks = (total + threads - 1) / threads;
+  hipLaunchKernelGGL(shard_endpoints_kernel,
+                     dim3(static_cast<uint32_t>(blocks), static_cast<uint32_t>(batch)),
+                     dim3(threads), 0, static_cast<hipStream_t>(stream), a);
+  return check_launch("shard_endpoints_kernel");
 }
 
 extern "C" int aspec_thd_row_metadata(const int64_t* anchors, const uint8_t* keep,

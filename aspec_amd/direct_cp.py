@@ -1,10 +1,13 @@
-"""Direct-CP / THD DSpark attention on MI355X (context-parallel degree 1).
+"""Direct-CP / THD DSpark attention on MI355X (context-parallel degree 1 end to end).
 
 Mirrors the operator surface of aspec/models/ops/direct_cp.py: `DirectCPMetadata` (147-262),
 `direct_cp_attention_from_kv` (1047-1100), `direct_cp_attention` (1027-1044),
-`build_context_positions` (23-53) and `direct_cp_attention_observation` (265-284). Every GPU
-backend name the reference accepts ("auto", "fa4", "cudnn_flex_attention") and "hip" run the same
-HIP kernels; the reference's CPU "math" backend is not part of this product.
+`build_context_positions` (23-53), `merge_attention_partials` (362-367) and
+`direct_cp_attention_observation` (265-284). Every GPU backend name the reference accepts ("auto",
+"fa4", "cudnn_flex_attention") and "hip" run the same HIP kernels; the reference's CPU "math"
+backend is not part of this product. With cp_size > 1 one rank's share of the work (all gathered
+queries against its context shard and its own draft blocks) runs through
+`direct_cp_partial_attention`; the collectives around it need several GPUs.
 """
 
 from __future__ import annotations
@@ -25,14 +28,27 @@ _GQA_MODES = {"auto", "native", "external", "internal"}
 
 def build_context_positions(total_positions: int, cp_rank: int, cp_size: int, *,
                             layout: str = "contiguous", alignment: int = 1) -> Tensor:
-    """Positions owned by one CP rank (direct_cp.py:23-53). One GPU: CP=1 owns arange(total)."""
+    """Positions owned by one CP rank (direct_cp.py:23-53): a contiguous shard
+    (`context_shard_bounds`, aligned groups), or for "zigzag" the chunks cp_rank and
+    2*cp_size - 1 - cp_rank of 2*cp_size equal chunks."""
     if total_positions < 0 or cp_size <= 0 or not 0 <= cp_rank < cp_size:
         raise ValueError("invalid context-parallel position layout")
     if layout not in {"contiguous", "zigzag"}:
         raise ValueError(f"unsupported context-parallel layout: {layout}")
-    if cp_size != 1:
-        raise NotImplementedError("context parallelism > 1 needs several GPUs; this build is CP=1")
-    return torch.arange(total_positions, dtype=torch.long)
+    if layout == "contiguous" or cp_size == 1:
+        from aspec_amd.collate import context_shard_bounds
+
+        start, end = context_shard_bounds(total_positions, cp_rank, cp_size, alignment=alignment)
+        return torch.arange(start, end, dtype=torch.long)
+    if alignment != 1:
+        raise ValueError("zigzag context ownership does not support aligned groups")
+    chunks = 2 * cp_size
+    owned = []
+    for chunk_rank in (cp_rank, chunks - 1 - cp_rank):
+        start = total_positions * chunk_rank // chunks
+        end = total_positions * (chunk_rank + 1) // chunks
+        owned.append(torch.arange(start, end, dtype=torch.long))
+    return torch.cat(owned)
 
 
 class _ForwardSparseCache:
@@ -136,11 +152,15 @@ class DirectCPMetadata:
 
     @property
     def local_block_ids(self) -> Tensor:
-        return torch.arange(self.num_blocks, dtype=torch.long)
+        """The blocks whose draft keys this rank holds (direct_cp.py:248-252)."""
+        return build_context_positions(self.num_blocks, self.cp_rank, self.cp_size, layout=self.layout)
 
     @property
     def collective_block_ids(self) -> Tensor:
-        return torch.arange(self.num_blocks, dtype=torch.long)
+        """Every rank's local blocks in rank order: the order of the gathered queries
+        (direct_cp.py:255-262)."""
+        return torch.cat([build_context_positions(self.num_blocks, rank, self.cp_size, layout=self.layout)
+                          for rank in range(self.cp_size)])
 
 
 def direct_cp_attention_observation(metadata: DirectCPMetadata) -> dict:
@@ -411,6 +431,105 @@ def dspark_attention(query: Tensor, key: Tensor, value: Tensor, metadata: Direct
     return output, lse
 
 
+def cp_shard_endpoints(metadata: DirectCPMetadata, device) -> Tensor:
+    """HIP `aspec_thd_cp_shard_endpoints`: the interval endpoints of this rank's partial
+    (`_build_cudnn_thd_mask` at cp_size > 1, direct_cp.py:750-878): every gathered query row (the
+    collective block order) against this rank's context shard and the draft keys of its own
+    blocks. Cached per forward; one host read of the layout flags, as the reference's monotonic
+    check (direct_cp.py:776-780)."""
+    device = torch.device(device)
+    key = ("hip_cp_shard_endpoints", device)
+    ends = metadata._fa4_cache.get(key)
+    if ends is not None:
+        return ends
+    batch, n, block, T = (metadata.anchor_positions.shape[0], metadata.num_blocks,
+                          metadata.block_size, metadata.context_length)
+    anchors = metadata.anchor_positions.to(device=device, dtype=torch.int64).contiguous()
+    keep = metadata.block_keep_mask.to(device=device, dtype=torch.bool).contiguous()
+    positions = metadata.context_position_ids.to(device=device, dtype=torch.int64).contiguous()
+    if metadata.context_doc_ids is None:
+        anchor_docs = torch.zeros((batch, n), dtype=torch.int64, device=device)
+        context_docs = torch.zeros((batch, T), dtype=torch.int64, device=device)
+    else:
+        anchor_docs = metadata.anchor_doc_ids.to(device=device, dtype=torch.int64).contiguous()
+        context_docs = metadata.context_doc_ids.to(device=device, dtype=torch.int64).contiguous()
+    query_blocks = metadata.collective_block_ids.to(device)
+    local_blocks = metadata.local_block_ids.to(device)
+    nq = query_blocks.numel() * block
+    ends = torch.empty((5, batch * nq), dtype=torch.int32, device=device)
+    flags = torch.zeros(1, dtype=torch.int32, device=device)
+    seq = metadata.sequence_length if metadata.sequence_length is not None else 0
+    with _timing.region("thd_row_metadata"):
+        _lib.call("aspec_thd_cp_shard_endpoints", _lib.ptr(anchors), _lib.ptr(keep), _lib.ptr(anchor_docs),
+                  _lib.ptr(positions), _lib.ptr(context_docs), batch, n, block, T, _lib.ptr(query_blocks),
+                  query_blocks.numel(), _lib.ptr(local_blocks), local_blocks.numel(), seq,
+                  metadata.context_window or 0, metadata.query_window or 0, int(metadata.draft_is_causal),
+                  _lib.ptr(ends), _lib.ptr(flags), _lib.stream_handle(device))
+    bad = int(flags.item())
+    if bad & 1:
+        raise ValueError("cuDNN THD requires monotonically ordered context positions")
+    if bad & 2:
+        raise ValueError("THD attention requires contiguous ascending documents (padding last)")
+    if bad & 4:
+        raise ValueError("CP block ownership out of range or not ascending")
+    metadata._fa4_cache[key] = ends
+    return ends
+
+
+def direct_cp_partial_attention(query_full: Tensor, key: Tensor, value: Tensor,
+                                metadata: DirectCPMetadata, scale: Optional[float] = None
+                                ) -> tuple[Tensor, Tensor]:
+    """One CP rank's partial attention, the step of direct_cp_attention_from_kv between the query
+    all-gather and the all-to-all of the partials (direct_cp.py:1077-1093): every gathered query
+    ([B, Hq, num_blocks * block_size, D] in the collective block order) against this rank's keys
+    ([B, Hkv, context_length + queries_per_rank, D]: its context shard, then its own blocks' draft
+    keys). Returns the partial (out, lse), each row normalised over this rank's keys only (rows
+    without a visible key here: O = 0, LSE = -1e30); `merge_attention_partials` combines the ranks'
+    partials exactly. Differentiable in query, key and value. The collectives around it need
+    several GPUs and are not part of this single-GPU build."""
+    length = metadata.context_length + metadata.queries_per_rank
+    if (key.ndim != 4 or value.ndim != 4 or key.shape[:3] != value.shape[:3]
+            or key.shape[0] != query_full.shape[0] or key.shape[2] != length):
+        raise ValueError("Combined KV must match local context and draft ownership")
+    if query_full.ndim != 4 or query_full.shape[2] != metadata.num_blocks * metadata.block_size:
+        raise ValueError(f"expected {metadata.num_blocks * metadata.block_size} gathered queries")
+    if not query_full.is_cuda:
+        raise ValueError("aspec_amd attention runs on the GPU; got a CPU tensor")
+    if query_full.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
+        raise NotImplementedError("aspec_amd DSpark attention computes in bf16 (fp32 accumulation)")
+    if query_full.shape[1] % key.shape[1]:
+        raise ValueError("query heads must be divisible by the matching KV head count")
+    if metadata.backend == "math":
+        raise NotImplementedError(
+            "the math backend is the reference's CPU path; aspec_amd runs the HIP kernels only")
+    scale = scale if scale is not None else query_full.shape[-1] ** -0.5
+    ends = cp_shard_endpoints(metadata, query_full.device)
+    batch = query_full.shape[0]
+    rows = ThdRows(None, None, ends, None, batch * query_full.shape[2], batch * key.shape[2], batch)
+    plan = attention_plan(metadata, rows, query_full.device)
+    if batch == 1:
+        return _DSparkAttention.apply(query_full, key, value, ends, plan, scale)
+    output, lse = _DSparkAttention.apply(_join_batch(query_full), _join_batch(key), _join_batch(value),
+                                         ends, plan, scale)
+    nq, hq = query_full.shape[2], query_full.shape[1]
+    output = output.transpose(1, 2).reshape(batch, nq, hq, output.shape[-1]).transpose(1, 2)
+    return output, lse[0].view(hq, batch, nq).permute(1, 0, 2)
+
+
+def merge_attention_partials(outputs: Tensor, lse_parts: Tensor) -> tuple[Tensor, Tensor]:
+    """Merge independently normalised attention partials exactly (`merge_attention_partials` /
+    `_merge_partials`, direct_cp.py:362-367,460-467): outputs [P, ..., D] and lse_parts [P, ...]
+    stacked over the P partials. lse = logsumexp over the partials, each partial weighted by
+    exp(lse_p - lse); a row none of whose partials is finite keeps LSE = -1e30. Differentiable."""
+    has_keys = torch.isfinite(lse_parts).any(dim=0)
+    safe_parts = torch.where(has_keys.unsqueeze(0), lse_parts, torch.zeros_like(lse_parts))
+    safe_lse = torch.logsumexp(safe_parts, dim=0)
+    lse = torch.where(has_keys, safe_lse, torch.full_like(safe_lse, MASK_VALUE))
+    weights = torch.exp(lse_parts - safe_lse.unsqueeze(0))
+    weights = torch.where(has_keys.unsqueeze(0), weights, torch.zeros_like(weights))
+    return (weights.unsqueeze(-1) * outputs).sum(dim=0), lse
+
+
 def direct_cp_attention_from_kv(query_own: Tensor, key: Tensor, value: Tensor,
                                 metadata: DirectCPMetadata, scale: Optional[float] = None, *,
                                 cudnn_gqa_mode: str = "auto") -> tuple[Tensor, Tensor]:
@@ -428,7 +547,10 @@ def direct_cp_attention_from_kv(query_own: Tensor, key: Tensor, value: Tensor,
         raise NotImplementedError(
             "the math backend is the reference's CPU path; aspec_amd runs the HIP kernels only")
     if metadata.cp_size != 1:
-        raise NotImplementedError("context parallelism > 1 needs several GPUs; this build is CP=1")
+        raise NotImplementedError(
+            "context parallelism > 1 gathers queries and exchanges partials between GPUs; this "
+            "single-GPU build runs one rank's share with direct_cp_partial_attention and combines "
+            "partials with merge_attention_partials")
     output, lse = dspark_attention(query_own, key, value, metadata, scale)
     return output.to(query_own.dtype), lse
 

@@ -244,8 +244,9 @@ class FusedBF16Optimizer:
     it returns the pre-clip gradient norm as a device scalar (no host synchronization) and, as the
     reference's step does, leaves every grad None. `zero_grad(set_to_none=False)` instead keeps every gradient as a view of one flat bf16 buffer
     that autograd accumulates into. With more than 64 trainable parameters, or one whose size is
-    not a multiple of 8, the gradients are gathered into that buffer and a grad of None counts as
-    zeros."""
+    not a multiple of 8, the gradients are gathered into that buffer and updated as one segment;
+    that path cannot skip a single parameter, so a step in which some parameter has no gradient
+    raises NotImplementedError there (the reference's AdamW would leave it untouched)."""
 
     def __init__(self, model, lr, weight_decay=0.0, max_grad_norm=0.5, total_steps=800_000,
                  warmup_ratio=0.015, decay_style="cosine", min_lr=0.0, betas=(0.9, 0.999), eps=1e-8):
@@ -342,16 +343,26 @@ class FusedBF16Optimizer:
                           self._seg_numel, len(self.params), *args)
             else:
                 # more than 64 parameters, or one whose size is not a multiple of 8: every gradient
-                # is gathered into the flat buffer (a grad of None counts as zeros there)
-                for p, off in zip(self.params, self._offsets()):
-                    view = self.grads[off:off + p.numel()].view_as(p)
-                    if p.grad is None:
-                        view.zero_()
-                    elif p.grad.data_ptr() != view.data_ptr():
-                        view.copy_(p.grad)
-                _lib.call("aspec_adamw_step", _lib.ptr(self.flat), _lib.ptr(self.master),
-                          _lib.ptr(self.exp_avg), _lib.ptr(self.exp_avg_sq), _lib.ptr(self.grads),
-                          self.flat.numel(), *args)
+                # is gathered into the flat buffer and the update runs as one segment, which has
+                # one step count and applies decay to every element, so a parameter without a
+                # gradient cannot be skipped as the reference's AdamW skips it (optimizer.py:99-109)
+                missing = sum(p.grad is None for p in self.params)
+                if 0 < missing < len(self.params):
+                    raise NotImplementedError(
+                        f"{missing} of {len(self.params)} trainable parameters have no gradient; the "
+                        "gathered AdamW path (more than 64 parameters, or a parameter whose size is "
+                        "not a multiple of 8) cannot skip them")
+                if missing == len(self.params):
+                    # nothing to update (every parameter is skipped); the norm of no gradients is 0
+                    self.grad_norm().zero_()
+                else:
+                    for p, off in zip(self.params, self._offsets()):
+                        view = self.grads[off:off + p.numel()].view_as(p)
+                        if p.grad.data_ptr() != view.data_ptr():
+                            view.copy_(p.grad)
+                    _lib.call("aspec_adamw_step", _lib.ptr(self.flat), _lib.ptr(self.master),
+                              _lib.ptr(self.exp_avg), _lib.ptr(self.exp_avg_sq), _lib.ptr(self.grads),
+                              self.flat.numel(), *args)
         self.last_step += 1
         for p in self.params:  # as the reference's step does: the gradients are consumed
             p.grad = None

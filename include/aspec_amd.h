@@ -80,6 +80,34 @@ int aspec_thd_batch_row_metadata(const int64_t* anchors, const uint8_t* keep,
                                  void* stream);
 
 /*
+ * Interval endpoints of one context-parallel rank's partial attention: the cp_size > 1 case of
+ * `_build_cudnn_thd_mask` (aspec/models/ops/direct_cp.py:750-878), whose visibility is `_visibility`
+ * (direct_cp.py:382-425). The queries are every block in the collective order query_blocks
+ * [num_query_blocks] (the ranks' `local_block_ids` concatenated, direct_cp.py:255-262), each expanded
+ * to block_size rows; the rank's keys are its context shard (context_positions / context_docs
+ * [batch][context_length], ascending positions, from `build_context_positions`) followed by the
+ * draft keys of its own blocks local_blocks [num_local_blocks] (ascending), block_size each. Query
+ * row q of block r sees the shard's context keys of its document before its anchor (windows as in
+ * aspec_thd_row_metadata) and, when this rank owns block r as local slot j, draft keys
+ * [T + j*B, T + j*B + valid); a block the rank does not own has both draft endpoints at the key
+ * length T + num_local_blocks*B, as the reference writes them. Dropped rows stay all zero.
+ * endpoints [5][batch * num_query_blocks * block_size] in the flattened key space (batch row b's keys
+ * at b*K). Bits of *status_flags (zeroed by the caller): 1 non-monotone context positions, 2
+ * non-monotone documents, 4 a block id out of range or local blocks not strictly ascending.
+ * The partial's attention runs through aspec_dspark_attn_fwd / _bwd with these endpoints; the
+ * ranks' (O, LSE) partials merge as in `_merge_partials` (direct_cp.py:460-467).
+ */
+int aspec_thd_cp_shard_endpoints(const int64_t* anchors, const uint8_t* keep,
+                                 const int64_t* anchor_docs, const int64_t* context_positions,
+                                 const int64_t* context_docs, int64_t batch, int64_t num_blocks,
+                                 int64_t block_size, int64_t context_length,
+                                 const int64_t* query_blocks, int64_t num_query_blocks,
+                                 const int64_t* local_blocks, int64_t num_local_blocks,
+                                 int64_t sequence_length, int64_t context_window,
+                                 int64_t query_window, int draft_is_causal, int32_t* endpoints,
+                                 int32_t* status_flags, void* stream);
+
+/*
  * Interval endpoints [5][Nq] recovered from the eight THD mask tensors (query_aux [4][Nq],
  * key_aux [4][K], the layout of `_query_metadata` / `_key_metadata` at CP=1, context keys first).
  * This is the input `_classify_tiles` consumes (aspec/models/ops/thd_sparse_metadata.py:20-94);

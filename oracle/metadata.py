@@ -1,6 +1,8 @@
 """Integer THD metadata oracle (numpy). TEST INFRASTRUCTURE ONLY -- see oracle/__init__.py.
 
-Everything is one packed row at context-parallel degree 1 (local blocks == all blocks).
+Everything is one packed row. The functions without a `cp_` prefix are context-parallel degree 1
+(local blocks == all blocks); `shard_positions`, `cp_math_visibility` and `cp_endpoints` restate
+one rank's share at cp_size > 1.
 """
 
 from __future__ import annotations
@@ -249,3 +251,113 @@ def visible_pairs(ends):
     tools/performance/bench_dspark_b7_attention.py:173-193)."""
     ends = np.asarray(ends, np.int64)
     return int(np.sum(ends[2] - ends[1]) + np.sum(ends[4] - ends[3]))
+
+
+def shard_positions(total, rank, cp, layout="contiguous", alignment=1):
+    """`build_context_positions` (direct_cp.py:23-53; the contiguous bounds are
+    `context_shard_bounds`, aspec/inference/context.py:30-55): int64 positions owned by `rank`."""
+    if layout == "contiguous" or cp == 1:
+        groups = total // alignment
+        start = groups * rank // cp * alignment
+        end = total if rank == cp - 1 else groups * (rank + 1) // cp * alignment
+        return np.arange(start, end, dtype=np.int64)
+    chunks = 2 * cp
+    parts = [np.arange(total * c // chunks, total * (c + 1) // chunks, dtype=np.int64)
+             for c in (rank, chunks - 1 - rank)]
+    return np.concatenate(parts)
+
+
+def cp_blocks(num_blocks, rank, cp, layout="contiguous"):
+    """(collective block order, this rank's local blocks): `collective_block_ids` and
+    `local_block_ids` (direct_cp.py:248-262)."""
+    collective = np.concatenate([shard_positions(num_blocks, r, cp, layout) for r in range(cp)])
+    return collective, shard_positions(num_blocks, rank, cp, layout)
+
+
+def cp_math_visibility(anchors, keep, anchor_docs, context_positions, context_docs, block,
+                       sequence_length, collective_blocks, local_blocks, context_window=None,
+                       query_window=None, draft_is_causal=False):
+    """`_visibility` (direct_cp.py:382-425) for one rank: [len(collective)*B, T_local + len(local)*B]
+    bool. Queries: the collective blocks' rows; keys: the rank's context positions (global
+    positions, with their documents), then its local blocks' draft keys."""
+    anchors = np.asarray(anchors, np.int64)
+    collective = np.asarray(collective_blocks, np.int64)
+    local = np.asarray(local_blocks, np.int64)
+    qblocks = np.repeat(collective, block)
+    qa = anchors[qblocks]
+    qkeep = token_keep(anchors[collective], np.asarray(keep, bool)[collective], block, sequence_length)
+    cpos = np.asarray(context_positions, np.int64)
+    vis_ctx = cpos[None, :] < qa[:, None]
+    if context_window is not None:
+        vis_ctx &= cpos[None, :] >= qa[:, None] - context_window
+    if context_docs is not None:
+        adocs = np.asarray(anchor_docs, np.int64)[qblocks]
+        cdocs = np.asarray(context_docs, np.int64)
+        vis_ctx &= (adocs[:, None] >= 0) & (cdocs[None, :] == adocs[:, None])
+    qoff = np.tile(np.arange(block), collective.size)
+    if query_window is not None:
+        vis_ctx &= (qa + qoff)[:, None] - cpos[None, :] < query_window
+    dblocks = np.repeat(local, block)
+    doff = np.tile(np.arange(block), local.size)
+    vis_draft = dblocks[None, :] == qblocks[:, None]
+    if draft_is_causal:
+        vis_draft &= doff[None, :] <= qoff[:, None]
+    if query_window is not None:
+        vis_draft &= np.abs(qoff[:, None] - doff[None, :]) < query_window
+    key_keep = np.concatenate([np.ones(cpos.size, bool),
+                               token_keep(anchors[local], np.asarray(keep, bool)[local], block, sequence_length)])
+    return np.concatenate([vis_ctx, vis_draft], axis=1) & qkeep[:, None] & key_keep[None, :]
+
+
+def cp_endpoints(anchors, keep, anchor_docs, context_positions, context_docs, block, sequence_length,
+                 collective_blocks, local_blocks, context_window=None, query_window=None,
+                 draft_is_causal=False):
+    """`_build_cudnn_thd_mask` (direct_cp.py:750-878) for one rank: int32 [5, len(collective)*B]
+    = (0, context_begin, context_end, draft_begin, draft_end) over the rank's keys; a block the
+    rank does not own has both draft endpoints at the key length; zeros on dropped rows."""
+    anchors = np.asarray(anchors, np.int64)
+    collective = np.asarray(collective_blocks, np.int64)
+    local = np.asarray(local_blocks, np.int64)
+    qblocks = np.repeat(collective, block)
+    offsets = np.tile(np.arange(block), collective.size)
+    qa = anchors[qblocks]
+    qkeep = token_keep(anchors[collective], np.asarray(keep, bool)[collective], block, sequence_length)
+    cpos = np.asarray(context_positions, np.int64)
+    T = cpos.size
+    key_length = T + local.size * block
+    lower = np.zeros_like(qa)
+    if context_window is not None:
+        lower = np.maximum(lower, qa - context_window)
+    if query_window is not None:
+        lower = np.maximum(lower, qa + offsets - query_window + 1)
+    cb = np.searchsorted(cpos, lower, side="left")
+    ce = np.searchsorted(cpos, qa, side="left")
+    if context_docs is not None:
+        cdocs = np.asarray(context_docs, np.int64)
+        adocs = np.asarray(anchor_docs, np.int64)[qblocks]
+        sortable = np.where(cdocs >= 0, cdocs, np.iinfo(np.int64).max)
+        cb = np.maximum(cb, np.searchsorted(sortable, adocs, side="left"))
+        ce = np.minimum(ce, np.searchsorted(sortable, adocs, side="right"))
+        qkeep = qkeep & (adocs >= 0)
+    cb = np.minimum(cb, ce)
+    slot_of = np.full(anchors.size, -1, np.int64)
+    slot_of[local] = np.arange(local.size)
+    slots = slot_of[qblocks]
+    owns = slots >= 0
+    base = T + np.maximum(slots, 0) * block
+    valid = np.full_like(qa, block)
+    if sequence_length is not None:
+        valid = np.clip(sequence_length - qa, 0, block)
+    db = base.copy()
+    de = base + valid
+    if draft_is_causal:
+        de = np.minimum(de, base + offsets + 1)
+    if query_window is not None:
+        db = base + np.clip(offsets - query_window + 1, 0, None)
+        de = np.minimum(de, base + np.clip(offsets + query_window, None, block))
+    db = np.minimum(db, de)
+    db = np.where(owns, db, key_length)
+    de = np.where(owns, de, key_length)
+    out = np.stack([np.zeros_like(cb), cb, ce, db, de])
+    out = np.where(qkeep[None, :], out, 0)
+    return out.astype(np.int32)

@@ -124,6 +124,52 @@ def test_fused_adamw_matches_oracle_with_clip_skip_and_missing_gradients(gpu):
     assert lrs == [warmup_decay_lr(i, max_lr=1e-2, total_steps=10, warmup_steps=2) for i in range(5)]
 
 
+class _OddParams(torch.nn.Module):
+    """A parameter of 37 elements ahead of another: the segment table needs multiples of 8, so the
+    optimizer takes its gathered path."""
+
+    def __init__(self, gpu):
+        super().__init__()
+        g = torch.Generator(device=gpu).manual_seed(13)
+        self.a = torch.nn.Parameter(torch.randn(37, device=gpu, generator=g).to(torch.bfloat16))
+        self.b = torch.nn.Parameter(torch.randn(513, device=gpu, generator=g).to(torch.bfloat16))
+
+
+def test_fused_adamw_gathered_path_matches_oracle_and_refuses_a_missing_gradient(gpu):
+    """The gathered path (a parameter whose size is not a multiple of 8): with every gradient
+    present it follows the optimizer oracle; a step in which one parameter has no gradient raises
+    NotImplementedError before any state changes (it cannot skip the parameter as the reference's
+    AdamW does); a step with no gradient at all leaves everything untouched."""
+    mod = _OddParams(gpu)
+    opt = FusedBF16Optimizer(mod, lr=1e-2, weight_decay=0.1, max_grad_norm=5.0, total_steps=10,
+                             warmup_ratio=0.0)
+    assert not opt._segments_ok
+    p0 = _np(torch.cat([mod.a.detach().reshape(-1), mod.b.detach().reshape(-1)]).float())
+    g = torch.Generator(device=gpu).manual_seed(14)
+    grads, lrs = [], []
+    for step in range(2):
+        ga = torch.randn(mod.a.shape, device=gpu, generator=g) * 0.05
+        gb = torch.randn(mod.b.shape, device=gpu, generator=g) * 0.05
+        ((mod.a * ga.to(torch.bfloat16)).sum() + (mod.b * gb.to(torch.bfloat16)).sum()).backward()
+        grads.append(_np(torch.cat([mod.a.grad.reshape(-1), mod.b.grad.reshape(-1)])))
+        lrs.append(opt.get_learning_rate())
+        norm = opt.step()
+        want_p, want_norms, _ = ol.adamw_steps(p0, grads, lrs=lrs, weight_decay=0.1, max_grad_norm=5.0)
+        assert float(norm) == pytest.approx(want_norms[-1], rel=1e-4)
+        np.testing.assert_allclose(_np(opt.master[: p0.size]), want_p[-1], rtol=1e-5, atol=1e-6)
+    master, exp_avg, state = opt.master.clone(), opt.exp_avg.clone(), opt.state.clone()
+    (mod.a.float().sum()).backward()  # b has no gradient
+    with pytest.raises(NotImplementedError, match="cannot skip"):
+        opt.step()
+    torch.cuda.synchronize()
+    assert torch.equal(opt.master, master) and torch.equal(opt.exp_avg, exp_avg)
+    assert torch.equal(opt.state, state)
+    opt.zero_grad()
+    before = _np(opt.master).copy()
+    assert float(opt.step()) == 0.0  # nothing to update
+    np.testing.assert_array_equal(_np(opt.master), before)
+
+
 def test_adamw_segments_match_the_flat_step_bit_for_bit(gpu):
     """aspec_adamw_step_segments over three gradient tensors (the last of odd size) against
     aspec_adamw_step over the same gradients gathered into one buffer, through the C ABI: master

@@ -1,8 +1,10 @@
 """aspec_qk_norm_rope_bwd_noalloc (the workspace-free Q/K norm + RoPE backward, its scratch a static
 device array) against aspec_qk_norm_rope_bwd with a caller-allocated workspace, through the C ABI:
 two calls in a row, the second with a smaller input, every output bitwise equal (the same
-deterministic kernels). Also: an invalid size is rejected, and torch's allocator is untouched by the
-workspace-free call."""
+deterministic kernels), for bf16 and fp16 activations. Also: an invalid size is rejected, and the
+workspace-free call allocates nothing at either level the process can observe: torch's caching
+allocator reserves no more memory, and the device's free memory as HIP reports it
+(hipMemGetInfo, through torch.cuda.mem_get_info) is the same before and after the call."""
 
 import ctypes
 
@@ -15,11 +17,13 @@ pytestmark = pytest.mark.gpu
 
 EPS = 1e-6
 BF16 = 4  # ASPEC_MASK_BF16
+F16 = 5  # ASPEC_MASK_F16
+DTYPES = {BF16: torch.bfloat16, F16: torch.float16}
 
 
-def _case(device, batch, lc, ld, hq, hkv, seed):
+def _case(device, batch, lc, ld, hq, hkv, seed, code=BF16):
     g = torch.Generator().manual_seed(seed)
-    bf = torch.bfloat16
+    bf = DTYPES[code]
     rnd = lambda *s: torch.randn(*s, generator=g).to(bf).to(device)  # noqa: E731
     x = dict(query=rnd(batch * ld, hq, 128), ctx=rnd(batch * lc, hkv, 128), drf=rnd(batch * ld, hkv, 128),
              wq=rnd(128), wk=rnd(128))
@@ -37,11 +41,12 @@ def _case(device, batch, lc, ld, hq, hkv, seed):
     _lib.call("aspec_qk_norm_rope_fwd", x["query"].data_ptr(), x["ctx"].data_ptr(), x["drf"].data_ptr(),
               x["wq"].data_ptr(), x["wk"].data_ptr(), x["cos"].data_ptr(), x["sin"].data_ptr(), 97, 128,
               x["pq"].data_ptr(), x["pc"].data_ptr(), x["pd"].data_ptr(), batch, lc, ld, hq, hkv, 128, EPS,
-              BF16, x["q_out"].data_ptr(), x["k_out"].data_ptr(), x["rstd_q"].data_ptr(), x["rstd_k"].data_ptr(),
+              code, x["q_out"].data_ptr(), x["k_out"].data_ptr(), x["rstd_q"].data_ptr(), x["rstd_k"].data_ptr(),
               flags.data_ptr(), stream)
     x["gq"] = rnd(batch * ld, hq, 128)
     x["gk"] = rnd(batch * (lc + ld), hkv, 128)
     x["sizes"] = (batch, lc, ld, hq, hkv)
+    x["code"] = code
     return x
 
 
@@ -57,7 +62,7 @@ def _args_head(x):
     return (x["gq"].data_ptr(), x["gk"].data_ptr(), x["query"].data_ptr(), x["ctx"].data_ptr(),
             x["drf"].data_ptr(), x["rstd_q"].data_ptr(), x["rstd_k"].data_ptr(), x["wq"].data_ptr(),
             x["wk"].data_ptr(), x["cos"].data_ptr(), x["sin"].data_ptr(), 97, 128, x["pq"].data_ptr(),
-            x["pc"].data_ptr(), x["pd"].data_ptr(), batch, lc, ld, hq, hkv, 128, EPS, BF16)
+            x["pc"].data_ptr(), x["pd"].data_ptr(), batch, lc, ld, hq, hkv, 128, EPS, x["code"])
 
 
 def _with_workspace(x):
@@ -76,18 +81,21 @@ def _without_workspace(x):
     out = _outputs(x)
     torch.cuda.synchronize()
     reserved = torch.cuda.memory_reserved()
+    free = torch.cuda.mem_get_info()[0]
     _lib.call("aspec_qk_norm_rope_bwd_noalloc", *_args_head(x), *(t.data_ptr() for t in out[:5]),
               out[5].data_ptr(), _lib.stream_handle(x["wq"].device))
     torch.cuda.synchronize()
     assert torch.cuda.memory_reserved() == reserved
+    assert torch.cuda.mem_get_info()[0] == free
     return out
 
 
-def test_noalloc_backward_equals_workspace_backward(gpu):
+@pytest.mark.parametrize("code", [BF16, F16])
+def test_noalloc_backward_equals_workspace_backward(gpu, code):
     # the first call fills the grid (2048 workgroups: the scratch's full size), the second is
     # smaller, so stale partials of the first call sit beyond the second call's groups
-    big = _case(gpu, 2, 2048, 512, 32, 8, seed=1)
-    small = _case(gpu, 1, 40, 24, 4, 2, seed=2)
+    big = _case(gpu, 2, 2048, 512, 32, 8, seed=1, code=code)
+    small = _case(gpu, 1, 40, 24, 4, 2, seed=2, code=code)
     for x in (big, small):
         want = _with_workspace(x)
         got = _without_workspace(x)
