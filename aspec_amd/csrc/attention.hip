@@ -124,6 +124,14 @@ struct TileOffsets {
   }
 };
 
+// A wave-uniform value behind an empty asm: the compiler keeps it in SGPRs as computed and cannot
+// rematerialize it (for instance by reloading a kernel argument inside a loop).
+template <typename T>
+__device__ __forceinline__ T opaque_s(T x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+
 __device__ __forceinline__ const char* byte_ptr(const uint16_t* p) { return reinterpret_cast<const char*>(p); }
 
 // The row-read half of TileOffsets alone, for kernels without register room for the other half.
@@ -970,15 +978,27 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   const RowOffsets ro(lane);
   const TrOffsets tro(lane);
 
-  const uint32_t qst2 = static_cast<uint32_t>(a.qst * 2), dost2 = static_cast<uint32_t>(a.dost * 2);
+  // The sources of this wave's stage loads are fixed for the whole walk: computed once and held in
+  // SGPRs, behind an empty asm so that the compiler cannot re-derive them from the kernel arguments
+  // inside the walk (each such reload is a scalar load whose wait also drains the wave's
+  // outstanding LDS reads). P waves load dO rows, dS waves Q rows and the row scalars.
+  const int64_t nq = opaque_s(a.nq);
+  const float scale_log2 = opaque_s(a.scale_log2);
+  const uint16_t* const rows_h0 = opaque_s(p_role ? a.dout + static_cast<int64_t>(hkv) * G * a.dosh
+                                                  : a.q + static_cast<int64_t>(hkv) * G * a.qsh);
+  const int64_t rows_tok = opaque_s(p_role ? a.dost : a.qst);
+  const int64_t rows_head = opaque_s(p_role ? a.dosh : a.qsh);
+  const uint32_t rows_tok2 = static_cast<uint32_t>(rows_tok * 2);
+  const float* const delta_h0 = opaque_s(a.ws_delta + static_cast<int64_t>(hkv) * G * a.nq);
+  const int32_t* const ends_w = a.ends + static_cast<int64_t>(max(w * 2 - 1, 0)) * nq;
   // Byte distance of the lanes 32-63 array: lse2 follows delta ([Hq][Nq] each), endpoint row e+1
   // follows row e.
   const uint32_t lane_half_ws = lane < 32 ? static_cast<uint32_t>(a.ws_lse2 - a.ws_delta) * 4u : 0u;
   const uint32_t lane_half_ends = lane < 32 ? 0u : static_cast<uint32_t>(a.nq) * 4u;
-  auto row_base = [&](int it, int64_t& q0, int& head, int& valid) __attribute__((always_inline)) {
+  auto row_base = [&](int it, int64_t& q0, int& h, int& valid) __attribute__((always_inline)) {
     q0 = static_cast<int64_t>(tile_entry(it / G) & ~kFullBit) * kBwdTileM;
-    head = hkv * G + it % G;
-    valid = static_cast<int>(min<int64_t>(kBwdTileM, a.nq - q0));
+    h = it % G;
+    valid = static_cast<int>(min<int64_t>(kBwdTileM, nq - q0));
   };
   // Loads of iteration `it` into a stage, split by role so that no wave queues behind the whole
   // stage in the CU's address unit: dS wave w moves Q rows 8w .. 8w+7 (and dS waves 0-2 the row
@@ -993,23 +1013,20 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   const bool three_loads = !p_role && w < 3;  // two row loads + one scalar load
   auto issue = [&](int it, KvStage& sb) __attribute__((always_inline)) {
     int64_t q0;
-    int head, valid;
-    row_base(it, q0, head, valid);
+    int h, valid;
+    row_base(it, q0, h, valid);
     const uint32_t ra = static_cast<uint32_t>(min(lrow_a, valid - 1));
     const uint32_t rb = static_cast<uint32_t>(min(lrow_b, valid - 1));
-    const uint16_t* rb_base = p_role ? a.dout + q0 * a.dost + head * a.dosh
-                                     : a.q + q0 * a.qst + head * a.qsh;
-    const uint32_t st2 = p_role ? dost2 : qst2;
+    const uint16_t* rb_base = rows_h0 + q0 * rows_tok + h * rows_head;
     uint16_t* dst = (p_role ? sb.dout : sb.q) + w * 8 * kRowLd;
-    lds_load16_at(rb_base, ra * st2 + lcol_a2, dst);
-    lds_load16_at(rb_base, rb * st2 + lcol_b2, dst + 4 * kRowLd);
+    lds_load16_at(rb_base, ra * rows_tok2 + lcol_a2, dst);
+    lds_load16_at(rb_base, rb * rows_tok2 + lcol_b2, dst + 4 * kRowLd);
     if (p_role) return;
     const uint32_t r4 = static_cast<uint32_t>(min(lane & 31, valid - 1)) * 4u;
     if (w == 0) {
-      lds_load4_at(a.ws_delta + static_cast<int64_t>(head) * a.nq + q0, r4 + lane_half_ws, sb.lse2);
+      lds_load4_at(delta_h0 + h * nq + q0, r4 + lane_half_ws, sb.lse2);
     } else if (w < 3) {
-      lds_load4_at(a.ends + static_cast<int64_t>(w * 2 - 1) * a.nq + q0, r4 + lane_half_ends,
-                   sb.ends[(w - 1) * 2]);
+      lds_load4_at(ends_w + q0, r4 + lane_half_ends, sb.ends[(w - 1) * 2]);
     }
   };
   // Before the barrier that ends trip i, this wave's loads of stage i+1 have landed; `later`
@@ -1056,10 +1073,10 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
     const bool live = i < iters;
     if constexpr (decltype(role)::value) {
       int64_t q0;
-      int head, valid;
-      row_base(i, q0, head, valid);
+      int h, valid;
+      row_base(i, q0, h, valid);
       const bool full = (tile_entry(i / G) & kFullBit) != 0;
-      dkdv_p_step(s_cur, x_cur, kvf, acc, pc, live, a.scale_log2, w, valid,
+      dkdv_p_step(s_cur, x_cur, kvf, acc, pc, live, scale_log2, w, valid,
                   full && valid == kBwdTileM, static_cast<int>(key0) + w * 32, ro, tro_t, lane);
     } else {
       dkdv_ds_step(s_cur, x_prv, kvf, acc, dc, live, w, ro, tro_t, lane);

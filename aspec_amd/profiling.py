@@ -9,11 +9,17 @@ one such group.
     python -m aspec_amd.profiling trace <kernel_trace.csv> [--md OUT] [--gaps NAME ...]
     python -m aspec_amd.profiling traffic --fetch <csv> --write <csv> --copy-fetch <csv>
                                           --copy-write <csv> --copy-mib MIB [--json OUT]
+    python -m aspec_amd.profiling counters <counter_collection.csv> ... [--match NAME ...] [--md OUT]
 
 `trace` prints per-group launch statistics and, for each `--gaps` pattern, the GPU-idle time
 before each matching dispatch (its start minus the latest end of every earlier dispatch).
 `traffic` turns FETCH_SIZE / WRITE_SIZE (KiB per dispatch) into bytes per launch, each scaled by
 what the same counter reads for a plain device copy of known size (`bench.py --copy-calibration`).
+`counters` averages SQ / GRBM counters per (kernel, grid) over one or more passes and derives:
+MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x GRBM_GUI_ACTIVE / XCDs), the share of the kernel's
+cycles an average SIMD's MFMA pipe is busy; VALU, SALU and LDS instructions per MFMA
+(SQ_INSTS_VALU counts the MFMAs too); the LDS bank-conflict rate; and the shares of the waves'
+resident cycles spent waiting for an LDS result or for anything.
 """
 
 from __future__ import annotations
@@ -134,6 +140,35 @@ def idle_gaps(dispatches, pattern: str, grid: int | None = None):
     return gaps
 
 
+def step_timeline(dispatches, marker: str, grid: int | None = None):
+    """Split the trace into steps at each dispatch matching `marker` (and `grid`) and report, per
+    step, the span from one marker dispatch to the next, the time at least one kernel ran (the
+    union of the dispatch intervals, so overlapping streams count once), the idle rest and the
+    three largest idle gaps with the kernel that followed each."""
+    starts = [i for i, d in enumerate(dispatches) if marker in d["name"] and (grid is None or d["grid"] == grid)]
+    steps = []
+    for a, b in zip(starts, starts[1:]):
+        seg = dispatches[a:b]
+        t0, t1 = seg[0]["start"], dispatches[b]["start"]
+        busy, cur_s, cur_e, gaps = 0, None, None, []
+        for d in sorted(seg, key=lambda x: x["start"]):
+            s0, e0 = d["start"], min(d["end"], t1)
+            if cur_e is None or s0 > cur_e:
+                if cur_e is not None:
+                    busy += cur_e - cur_s
+                    gaps.append(((s0 - cur_e) / 1e3, d["name"]))
+                cur_s, cur_e = s0, e0
+            else:
+                cur_e = max(cur_e, e0)
+        busy += cur_e - cur_s
+        if t1 > cur_e:
+            gaps.append(((t1 - cur_e) / 1e3, dispatches[b]["name"]))
+        gaps.sort(key=lambda g: -g[0])
+        steps.append({"span_us": (t1 - t0) / 1e3, "busy_us": busy / 1e3, "idle_us": (t1 - t0 - busy) / 1e3,
+                      "largest_gaps": [(round(g, 1), n[:48]) for g, n in gaps[:3]]})
+    return steps
+
+
 def counter_per_dispatch(path, counter: str):
     """{(name, grid): [value per dispatch]} of one counter from a counter_collection.csv."""
     out = defaultdict(list)
@@ -178,6 +213,62 @@ def traffic(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, copy_mib):
             "regions": regions, "kernels": kernels}
 
 
+MI355X_SIMDS, MI355X_XCDS = 1024, 8
+
+
+def counter_summary(paths, match=()):
+    """{group: {counter: mean per dispatch}} over counter_collection CSVs (several passes of the
+    same program), restricted to kernels whose name contains one of `match` (all when empty)."""
+    sums = defaultdict(lambda: defaultdict(list))
+    for path in paths:
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                name = short_name(r["Kernel_Name"])
+                if match and not any(m in name for m in match):
+                    continue
+                sums[group_key(name, _grid(r))][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    return {k: {c: sum(v) / len(v) for c, v in d.items()} for k, d in sums.items()}
+
+
+def counters_markdown(summary):
+    def ratio(d, a, b, scale=1.0):
+        return d[a] / (d[b] * scale) if a in d and b in d and d[b] else float("nan")
+
+    lines = ["| kernel [grid] | GRBM cycles/XCD | MFMA busy | VALU per MFMA | SALU per MFMA | "
+             "LDS per MFMA | LDS bank conflicts | LDS wait share | any-wait share |",
+             "|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for k, d in sorted(summary.items(), key=lambda kv: -kv[1].get("GRBM_GUI_ACTIVE", 0)):
+        gui = d.get("GRBM_GUI_ACTIVE", float("nan"))
+        busy = d["SQ_VALU_MFMA_BUSY_CYCLES"] / (MI355X_SIMDS * gui / MI355X_XCDS) if "SQ_VALU_MFMA_BUSY_CYCLES" in d else float("nan")
+        lines.append(f"| `{k[:80]}` | {gui / MI355X_XCDS:.0f} | {busy:.3f} | {ratio(d, 'SQ_INSTS_VALU', 'SQ_INSTS_MFMA'):.2f} | "
+                     f"{ratio(d, 'SQ_INSTS_SALU', 'SQ_INSTS_MFMA'):.2f} | {ratio(d, 'SQ_INSTS_LDS', 'SQ_INSTS_MFMA'):.2f} | "
+                     f"{ratio(d, 'SQ_LDS_BANK_CONFLICT', 'SQ_LDS_IDX_ACTIVE'):.4f} | "
+                     f"{ratio(d, 'SQ_WAIT_INST_LDS', 'SQ_WAVE_CYCLES'):.3f} | {ratio(d, 'SQ_WAIT_ANY', 'SQ_WAVE_CYCLES'):.3f} |")
+    lines += ["", "Raw means per dispatch:", ""]
+    for k, d in sorted(summary.items()):
+        lines.append(f"- `{k[:80]}`: " + ", ".join(f"{c} {v:.4g}" for c, v in sorted(d.items())))
+    return "\n".join(lines)
+
+
+def traffic_markdown(out, top=20):
+    cal = out["calibration"]
+    lines = [f"Calibration: a {cal['copy_mib']} MiB device copy gives {cal['fetch_factor']:.4f} bytes per FETCH_SIZE "
+             f"byte-unit and {cal['write_factor']:.4f} per WRITE_SIZE byte-unit (KiB counters x 1024 x factor).", "",
+             "| bench region | dispatch group | HBM read MB | HBM write MB |", "|---|---|---:|---:|"]
+    for region, r in out["regions"].items():
+        rd = "" if r["read_bytes"] is None else f"{r['read_bytes'] / 1e6:.1f}"
+        wr = "" if r["write_bytes"] is None else f"{r['write_bytes'] / 1e6:.1f}"
+        lines.append(f"| {region} | `{r['group'][:80]}` | {rd} | {wr} |")
+    lines += ["", f"All dispatch groups, largest traffic first (top {top}):", "",
+              "| dispatch group | launches | HBM read MB | HBM write MB |", "|---|---:|---:|---:|"]
+    rows = sorted(out["kernels"].items(), key=lambda kv: -((kv[1]["read_bytes"] or 0) + (kv[1]["write_bytes"] or 0)))
+    for k, r in rows[:top]:
+        rd = "" if r["read_bytes"] is None else f"{r['read_bytes'] / 1e6:.1f}"
+        wr = "" if r["write_bytes"] is None else f"{r['write_bytes'] / 1e6:.1f}"
+        lines.append(f"| `{k[:90]}` | {r['calls']} | {rd} | {wr} |")
+    return "\n".join(lines)
+
+
 def trace_markdown(dispatches, gap_patterns=(), phases=None):
     stats = kernel_stats(dispatches)
     total = sum(s["total_us"] for s in stats.values())
@@ -213,18 +304,41 @@ def main(argv=None):
     t.add_argument("--md")
     t.add_argument("--gaps", nargs="*", default=[],
                    help="kernel-name patterns (optionally NAME@GRID) whose preceding idle time is reported")
+    t.add_argument("--steps-at", default="",
+                   help="NAME[@GRID] of a kernel launched once per step: per-step span, busy and idle time")
     t.add_argument("--phases", default="",
                    help="consecutive phases of steps as LABEL:COUNT,... (bench.py --serial --steps S "
                         "--warmup W: warmup:W,timed:S,timing-warmup:1,timing:S)")
+    q = sub.add_parser("counters")
+    q.add_argument("csv", nargs="+")
+    q.add_argument("--match", nargs="*", default=[])
+    q.add_argument("--md")
     c = sub.add_parser("traffic")
     for name in ("fetch", "write", "copy-fetch", "copy-write"):
         c.add_argument(f"--{name}", required=True)
     c.add_argument("--copy-mib", type=int, required=True)
     c.add_argument("--json")
+    c.add_argument("--md")
     args = p.parse_args(argv)
     if args.cmd == "trace":
         phases = [(p.split(":")[0], int(p.split(":")[1])) for p in args.phases.split(",") if p]
-        text = trace_markdown(load_dispatches(args.csv), args.gaps, phases or None)
+        dispatches = load_dispatches(args.csv)
+        text = trace_markdown(dispatches, args.gaps, phases or None)
+        if args.steps_at:
+            name, _, grid = args.steps_at.partition("@")
+            steps = step_timeline(dispatches, name, int(grid) if grid else None)
+            text += ("\n\nPer step (from one `" + args.steps_at + "` dispatch to the next):\n\n"
+                     "| step | span us | busy us | idle us | largest idle gaps (us, next kernel) |\n"
+                     "|---:|---:|---:|---:|---|\n")
+            for i, st in enumerate(steps):
+                gaps = "; ".join(f"{g} before `{n}`" for g, n in st["largest_gaps"])
+                text += f"| {i} | {st['span_us']:.1f} | {st['busy_us']:.1f} | {st['idle_us']:.1f} | {gaps} |\n"
+        if args.md:
+            with open(args.md, "w") as f:
+                f.write(text + "\n")
+        print(text)
+    elif args.cmd == "counters":
+        text = counters_markdown(counter_summary(args.csv, args.match))
         if args.md:
             with open(args.md, "w") as f:
                 f.write(text + "\n")
@@ -235,7 +349,10 @@ def main(argv=None):
         if args.json:
             with open(args.json, "w") as f:
                 f.write(text + "\n")
-        print(text)
+        if args.md:
+            with open(args.md, "w") as f:
+                f.write(traffic_markdown(out) + "\n")
+        print(text if not args.md else traffic_markdown(out))
 
 
 if __name__ == "__main__":

@@ -88,6 +88,10 @@ def parse():
     p.add_argument("--layer-step-only", action="store_true",
                    help="only time the config-5 one-layer training step and print its JSON object "
                         "(for profiling it on its own)")
+    p.add_argument("--attention-only", default="", metavar="WORKLOAD",
+                   help="only run attention forward + backward of one workload (config1, config2, "
+                        "config3_bin0, config3_bin1, config4, reference_b7), --warmup + --steps "
+                        "times on one stream, and print its JSON object (for rocprofv3 passes)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (5 times): the reference kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -377,6 +381,38 @@ def attention_timing(w, device, reps, flush):
     del run
     torch.cuda.empty_cache()
     return out
+
+
+WORKLOADS = {"config1": lambda W: W.config1(0), "config2": lambda W: W.config2(),
+             "config3_bin0": lambda W: W.config3(0, 0), "config3_bin1": lambda W: W.config3(0, 1),
+             "config4": lambda W: W.config4(), "reference_b7": lambda W: W.reference_b7()}
+
+
+def attention_only(device, name, steps, warmup):
+    """Attention forward + backward of one workload, one stream (dQ after dK/dV), for profiling:
+    `warmup` untimed and `steps` timed calls; mean wall milliseconds per call."""
+    import torch
+
+    from aspec_amd import workloads as W
+    from aspec_amd.direct_cp import backward_overlap, set_backward_overlap
+
+    if name not in WORKLOADS:
+        raise SystemExit(f"unknown workload {name!r}; one of {sorted(WORKLOADS)}")
+    w = WORKLOADS[name](W)
+    overlap = backward_overlap()
+    set_backward_overlap(False)
+    run = AttentionRunner(w, device)
+    for _ in range(warmup):
+        run.combined()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run.combined()
+    torch.cuda.synchronize()
+    set_backward_overlap(overlap)
+    return {"workload": name, "steps": steps, "warmup": warmup,
+            "ms_per_fwd_bwd": round((time.perf_counter() - t0) * 1e3 / max(steps, 1), 4),
+            "visible_pairs_per_head": visible_pairs(w, device)}
 
 
 def config1_cpu_ms(w, seed=0):
@@ -866,6 +902,10 @@ def main():
     device = torch.device("cuda:0")
     if args.layer_step_only:
         print(json.dumps({"config5_layer_step": layer_step(device, args.steps, args.warmup)}), flush=True)
+        return
+    if args.attention_only:
+        print(json.dumps({"attention_only": attention_only(device, args.attention_only, args.steps,
+                                                           args.warmup)}), flush=True)
         return
     x = build_inputs(device, args.seed)
     head_fn = _Head.make()
