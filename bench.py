@@ -30,9 +30,10 @@ After the main measurement attention forward + backward alone is timed under "at
 config 1 also with the CPU math path's milliseconds) and on the reference's own published workload
 (B = 7, 10 x 4096 + 40960 + 49152 context tokens, 6144 anchors; tests/golden/dspark_b7_workload.json)
 beside the reference's SM100 figures. Those timings follow the reference's kernel-benchmark
-contract (tools/performance/bench_dspark_b7_attention.py:196-243): a 256 MiB cache flush before
-each window of 10 calls, 11 windows, the first 2 discarded, median of 9; forward, backward and
-both separately. The full one-layer DSpark training step of BASELINE config 5 (forward, loss,
+contract (tools/performance/bench_dspark_b7_attention.py:196-243; docs/dspark_attn_kernel_optimization.md:159):
+forward, backward and both, each captured once in a HIP graph; a 256 MiB cache flush before each
+window of 10 graph replays, 11 windows, the first 2 discarded, median of 9. The same F+B launched
+from the host is reported beside it. The full one-layer DSpark training step of BASELINE config 5 (forward, loss,
 backward and the fused AdamW) is timed on its own and reported under "config5_layer_step" (skip
 with --no-layer-step).
 After the timed work, "parity" compares the HIP outputs with the oracle on the bench's own
@@ -92,6 +93,9 @@ def parse():
                    help="only run attention forward + backward of one workload (config1, config2, "
                         "config3_bin0, config3_bin1, config4, reference_b7), --warmup + --steps "
                         "times on one stream, and print its JSON object (for rocprofv3 passes)")
+    p.add_argument("--attention-configs-only", action="store_true",
+                   help="only time attention alone at every workload under the kernel-bench "
+                        "contract (the attention_configs object, without the config-1 CPU leg)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (5 times): the reference kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -331,6 +335,38 @@ class AttentionRunner:
 
         return torch.autograd.grad(self.forward(), (self.q, self.k, self.v), self.dout)
 
+    def capture(self):
+        """Forward, backward and forward + backward each captured once in a HIP graph, the way the
+        reference times its routes (captured fixed-shape forward and backward replayed,
+        bench_dspark_b7_attention.py:654-696). Everything runs on one stream S: the eager forward
+        whose autograd graph the backward capture replays, the warm-up and the captures, so each
+        backward node launches on S (autograd runs a node's backward on its forward's stream) and
+        dQ's second stream forks from S and joins it again inside the capture. Returns
+        {phase: (graph, outputs)}; a replay reruns the captured kernels on the same buffers.
+        Q/K/V become fresh leaves (same storage) first: a leaf's gradient-accumulator node keeps
+        the stream of the forward that created it while any graph through it lives, and one made
+        by an earlier forward on the default stream would join that stream into the capture."""
+        import torch
+
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        self.prepared = None
+        self.q, self.k, self.v = (x.detach().requires_grad_() for x in (self.q, self.k, self.v))
+        with torch.cuda.stream(stream):
+            for _ in range(2):
+                self.combined()
+            self.prepare_backward()
+            self.backward()
+        stream.synchronize()
+        graphs = {}
+        for phase, fn in (("fwd", self.forward), ("bwd", self.backward), ("fb", self.combined)):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                outputs = fn()
+            graphs[phase] = (graph, outputs)
+        torch.cuda.current_stream().wait_stream(stream)
+        return graphs
+
 
 ATTN_KERNELS = ("attn_fwd", "attn_bwd_prepare", "attn_bwd_dq", "attn_bwd_dkdv", "attn_bwd_finalize")
 
@@ -348,8 +384,11 @@ def attention_timing(w, device, reps, flush):
         run.combined()
     run.prepare_backward()
     torch.cuda.synchronize()
-    times = {"fwd": contract_ms(run.forward, flush), "bwd": contract_ms(run.backward, flush),
-             "fb": contract_ms(run.combined, flush)}
+    host_fb = contract_ms(run.combined, flush)
+    graphs = run.capture()
+    times = {p: contract_ms(g.replay, flush) for p, (g, _) in graphs.items()}
+    del graphs
+    torch.cuda.synchronize()
     overlap = backward_overlap()
     set_backward_overlap(False)
     _timing.reset()
@@ -370,6 +409,7 @@ def attention_timing(w, device, reps, flush):
         "visible_pairs_per_head": pairs, "gflop": {p: round(f / 1e9, 1) for p, f in flops.items()},
         "contract_ms": {p: {k: v for k, v in t.items() if k != "samples_ms"} for p, t in times.items()},
         "contract_samples_ms": {p: t["samples_ms"] for p, t in times.items()},
+        "host_launched_fb_ms": {k: v for k, v in host_fb.items() if k != "samples_ms"},
         "tflops": {p: round(flops[p] / (times[p]["median_ms"] * 1e-3) / 1e12, 2) for p in flops},
         "kernels_ms": {n: round(st[n]["mean_ms"], 4) for n in ATTN_KERNELS},
         "isolated_fwd_bwd_ms": round(iso, 4),
@@ -453,8 +493,10 @@ def attention_configs(device, reps, include_cpu=True):
 
     flush = flush_buffer(device)
     out = {"contract": dict(CONTRACT, scope="attention forward / backward / both through "
-                                            "direct_cp_attention_from_kv; plan built once per "
-                                            "forward and reused; host-launched replays")}
+                                            "direct_cp_attention_from_kv, each captured in a HIP "
+                                            "graph and replayed; plan built once per forward and "
+                                            "reused; host_launched_fb_ms: the same F+B launched "
+                                            "from the host")}
     for w in (W.config1(0), W.config2(), W.config3(0, 0), W.config3(0, 1), W.config4(), W.reference_b7()):
         out[w.name] = attention_timing(w, device, reps, flush)
     c1 = out["config1"]
@@ -906,6 +948,9 @@ def main():
     if args.attention_only:
         print(json.dumps({"attention_only": attention_only(device, args.attention_only, args.steps,
                                                            args.warmup)}), flush=True)
+        return
+    if args.attention_configs_only:
+        print(json.dumps({"attention_configs": attention_configs(device, 10, include_cpu=False)}), flush=True)
         return
     x = build_inputs(device, args.seed)
     head_fn = _Head.make()
