@@ -96,7 +96,8 @@ class _SpanTable:
         if not self.rows:
             return
         table = torch.from_numpy(np.concatenate(self.rows)).to(device)
-        _lib.call("aspec_pack_copy", table.data_ptr(), table.shape[0], _lib.stream_handle(device))
+        with _timing.region("pack_copy"):
+            _lib.call("aspec_pack_copy", table.data_ptr(), table.shape[0], _lib.stream_handle(device))
 
 
 class DFlashPackingCollator:

@@ -48,7 +48,7 @@ REGION_GROUPS = {
     "teacher_gemm": ("Cijk_Alik_Bljk_BBS_BH_MT256x256x64_MI16x16x1_UserArgs_shortname1", 512000),
     "qk_norm_rope_fwd": ("qk_norm_rope_fwd_kernel<false>", None),
     "qk_norm_rope_bwd": ("qk_norm_rope_bwd_kernel<false>", None),
-    "pack_row": ("pack_copy_kernel", None),
+    "pack_copy": ("pack_copy_kernel", None),
 }
 
 

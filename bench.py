@@ -610,6 +610,7 @@ def aux_rows(device, w, reps):
     moved = sum(feat[k].numel() * feat[k].element_size() for k in
                 ("input_ids", "loss_mask", "hidden_states", "last_hidden_states"))
     work = {"pack_row": 2 * moved + T * 8 * 3,                 # read + write every field, 3 metadata rows
+            "pack_copy": 2 * moved,                            # the copy kernel alone
             "anchor_sample": T * (8 + 8 + 4) + w.num_blocks * 9}  # mask, docs, compacted list; outputs
     return {k: (stats[k]["mean_ms"], stats[k]["launches"], work[k]) for k in work if k in stats}
 
