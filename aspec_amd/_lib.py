@@ -41,7 +41,7 @@ SIGNATURES = {
         _int,
         [_c_void_p, _i64, _i64] * 3
         + [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32, _c_void_p, _i64, _i64,
-           _c_void_p, _c_void_p],
+           _c_void_p, _int, _c_void_p],
     ),
     "aspec_dspark_attn_bwd_workspace_bytes": (_int, [_i64, _i64, _i64, _i64, _size_p]),
     "aspec_dspark_attn_bwd": (
@@ -49,7 +49,7 @@ SIGNATURES = {
         [_c_void_p, _i64, _i64] * 5
         + [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32]
         + [_c_void_p, _i64, _i64] * 3
-        + [_c_void_p, _c_void_p],
+        + [_c_void_p, _int, _c_void_p],
     ),
     "aspec_dspark_attn_bwd_stages": (
         _int,
@@ -57,7 +57,7 @@ SIGNATURES = {
         + [_c_void_p, _i64, _i64] * 5
         + [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32]
         + [_c_void_p, _i64, _i64] * 3
-        + [_c_void_p, _c_void_p],
+        + [_c_void_p, _int, _c_void_p],
     ),
     "aspec_loss_stats_floats": (_int, []),
     "aspec_ce_l1_fwd": (
@@ -129,7 +129,7 @@ SIGNATURES = {
     "aspec_pack_work_aware_rows": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64] + [_c_void_p] * 3),
 }
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 _lock = threading.Lock()
 _lib = None

@@ -79,7 +79,7 @@ __device__ __forceinline__ void load_row_frag(bf16x8 (&frag)[8], const uint16_t*
 // Two independent 8-step chains: acc0 = A0 x B0, acc1 = A1 x B1 over the 128-dim reduction. A rows
 // live in LDS (`ra0` / `ra1`), read AHEAD k-steps ahead of their MFMA; the B operands come from
 // registers.
-template <int AHEAD, typename Operand>
+template <int AHEAD, bool F16 = false, typename Operand>
 __device__ __forceinline__ void mfma_chains2(f32x16& acc0, f32x16& acc1, const Operand& ra0,
                                              const Operand& ra1, const bf16x8 (&b0)[8],
                                              const bf16x8 (&b1)[8]) {
@@ -97,8 +97,8 @@ __device__ __forceinline__ void mfma_chains2(f32x16& acc0, f32x16& acc1, const O
       x0[ds + AHEAD] = ra0.step(ds + AHEAD);
       x1[ds + AHEAD] = ra1.step(ds + AHEAD);
     }
-    acc0 = mfma32(as_bf16x8(x0[ds]), b0[ds], acc0);
-    acc1 = mfma32(as_bf16x8(x1[ds]), b1[ds], acc1);
+    acc0 = mfma32<F16>(as_bf16x8(x0[ds]), b0[ds], acc0);
+    acc1 = mfma32<F16>(as_bf16x8(x1[ds]), b1[ds], acc1);
     ASPEC_STEP_FENCE();
   }
 }
@@ -173,7 +173,7 @@ __device__ __forceinline__ bf16x8 read_tr_t(const uint16_t* tile, const TileOffs
 
 // acc[d] += A(d, ks) x B[ks] as mfma_tr_blocks, with the fragments read through TileOffsets;
 // `cur` holds k-step 0.
-template <int KS>
+template <int KS, bool F16 = false>
 __device__ __forceinline__ void mfma_tr_blocks_t(f32x16 (&acc)[4], const uint16_t* tile,
                                                  const TileOffsets& o, bf16x8 (&cur)[4],
                                                  const bf16x8 (&b)[KS]) {
@@ -185,7 +185,7 @@ __device__ __forceinline__ void mfma_tr_blocks_t(f32x16 (&acc)[4], const uint16_
       for (int d = 0; d < 4; ++d) nxt[d] = read_tr_t(tile, o, ks + 1, d);
     }
 #pragma unroll
-    for (int d = 0; d < 4; ++d) acc[d] = mfma32(cur[d], b[ks], acc[d]);
+    for (int d = 0; d < 4; ++d) acc[d] = mfma32<F16>(cur[d], b[ks], acc[d]);
     ASPEC_STEP_FENCE();
     if (ks + 1 < KS) {
 #pragma unroll
@@ -194,19 +194,28 @@ __device__ __forceinline__ void mfma_tr_blocks_t(f32x16 (&acc)[4], const uint16_
   }
 }
 
-// Sum of the 32 bf16 values of four packed operands (the rounded P that the P.V MFMAs use), two
-// at a time with the bf16 dot product against ones.
-__device__ __forceinline__ float sum_bf16(const bf16x8 (&pb)[4]) {
+// Sum of the 32 values of four packed operands (the rounded P that the P.V MFMAs use), two at a
+// time with the bf16 (fp16) dot product against ones.
+template <bool F16 = false>
+__device__ __forceinline__ float sum_p(const bf16x8 (&pb)[4]) {
   typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2v;
-  const bf16x2v ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
   float acc0 = 0.f, acc1 = 0.f;
+  auto dot = [](uint32_t w, float acc) __attribute__((always_inline)) {
+    if constexpr (F16) {
+      const f16x2_t ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+      return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), ones, acc, false);
+    } else {
+      const bf16x2v ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+      return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, w), ones, acc, false);
+    }
+  };
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint4 v = __builtin_bit_cast(uint4, pb[i]);
-    acc0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.x), ones, acc0, false);
-    acc1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.y), ones, acc1, false);
-    acc0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.z), ones, acc0, false);
-    acc1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, v.w), ones, acc1, false);
+    acc0 = dot(v.x, acc0);
+    acc1 = dot(v.y, acc1);
+    acc0 = dot(v.z, acc0);
+    acc1 = dot(v.w, acc1);
   }
   return acc0 + acc1;
 }
@@ -222,7 +231,7 @@ __device__ __forceinline__ void read_tr_first(bf16x8 (&cur)[4], const uint16_t* 
 // transposed fragment of the row-major LDS `tile` (rows = the reduction index, 16 per k-step;
 // columns d*32 .. +32 = the output rows), read with transpose loads; `cur` holds k-step 0
 // (read_tr_first).
-template <int KS>
+template <int KS, bool F16 = false>
 __device__ __forceinline__ void mfma_tr_blocks(f32x16 (&acc)[4], const uint16_t* tile,
                                                const TrOffsets& tro, bf16x8 (&cur)[4],
                                                const bf16x8 (&b)[KS]) {
@@ -234,7 +243,7 @@ __device__ __forceinline__ void mfma_tr_blocks(f32x16 (&acc)[4], const uint16_t*
       for (int d = 0; d < 4; ++d) nxt[d] = read_tr_operand(tile, tro, (ks + 1) * 16, d * 32);
     }
 #pragma unroll
-    for (int d = 0; d < 4; ++d) acc[d] = mfma32(cur[d], b[ks], acc[d]);
+    for (int d = 0; d < 4; ++d) acc[d] = mfma32<F16>(cur[d], b[ks], acc[d]);
     ASPEC_STEP_FENCE();
     if (ks + 1 < KS) {
 #pragma unroll
@@ -243,14 +252,15 @@ __device__ __forceinline__ void mfma_tr_blocks(f32x16 (&acc)[4], const uint16_t*
   }
 }
 
+template <bool F16 = false>
 __device__ __forceinline__ void store_row_c(uint16_t* dst, const f32x16 (&acc)[4], float mul, int g) {
 #pragma unroll
   for (int db = 0; db < 4; ++db) {
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
       u32x2 w;
-      w.x = pack_bf16x2(acc[db][rq * 4 + 0] * mul, acc[db][rq * 4 + 1] * mul);
-      w.y = pack_bf16x2(acc[db][rq * 4 + 2] * mul, acc[db][rq * 4 + 3] * mul);
+      w.x = pack_elem2<F16>(acc[db][rq * 4 + 0] * mul, acc[db][rq * 4 + 1] * mul);
+      w.y = pack_elem2<F16>(acc[db][rq * 4 + 2] * mul, acc[db][rq * 4 + 3] * mul);
       *reinterpret_cast<u32x2*>(dst + db * 32 + rq * 8 + g * 4) = w;
     }
   }
@@ -371,6 +381,7 @@ struct ListWindow {
 // Online softmax of one 64-key tile of scores S^T (`s`, lane = query row): masks a partial tile,
 // raises the running maximum (rescaling O and the row sum only when it grows by more than
 // kRescaleThreshold), and leaves P, rounded to bf16, in `pb` as the P.V operand.
+template <bool F16>
 __device__ __forceinline__ void fwd_softmax(f32x16 (&s)[2], f32x16 (&oacc)[4], float& m_run,
                                             float& l_run, bool partial, const RowIntervals& iv,
                                             float scale_log2, int g, bf16x8 (&pb)[4]) {
@@ -404,33 +415,34 @@ __device__ __forceinline__ void fwd_softmax(f32x16 (&s)[2], f32x16 (&oacc)[4], f
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[kb][r] = fast_exp2(fmaf(s[kb][r], scale_log2, neg_m));
   }
-  pb[0] = pack_c_half(s[0], 0);
-  pb[1] = pack_c_half(s[0], 8);
-  pb[2] = pack_c_half(s[1], 0);
-  pb[3] = pack_c_half(s[1], 8);
+  pb[0] = pack_c_half<F16>(s[0], 0);
+  pb[1] = pack_c_half<F16>(s[0], 8);
+  pb[2] = pack_c_half<F16>(s[1], 0);
+  pb[3] = pack_c_half<F16>(s[1], 8);
   // The row sum is taken over the rounded P that the P.V product uses, so O is normalized by
   // exactly the weights it was built from.
-  l_run += sum_bf16(pb);
+  l_run += sum_p<F16>(pb);
 }
 
+template <bool F16>
 __device__ __forceinline__ void fwd_tile(const uint16_t* sk, const uint16_t* sv,
                                          const bf16x8 (&qf)[8], f32x16 (&oacc)[4], float& m_run,
                                          float& l_run, bool partial, const RowIntervals& iv, float scale_log2,
                                          const TileOffsets& o, int g) {
   f32x16 s[2];
-  mfma_chains2<kFwdAhead>(s[0], s[1], RowOperandT{sk, o}, RowOperandT{sk + 32 * kRowLd, o}, qf, qf);
+  mfma_chains2<kFwdAhead, F16>(s[0], s[1], RowOperandT{sk, o}, RowOperandT{sk + 32 * kRowLd, o}, qf, qf);
   bf16x8 vcur[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) vcur[d] = read_tr_t(sv, o, 0, d);
   bf16x8 pb[4];
-  fwd_softmax(s, oacc, m_run, l_run, partial, iv, scale_log2, g, pb);
-  mfma_tr_blocks_t<4>(oacc, sv, o, vcur, pb);
+  fwd_softmax<F16>(s, oacc, m_run, l_run, partial, iv, scale_log2, g, pb);
+  mfma_tr_blocks_t<4, F16>(oacc, sv, o, vcur, pb);
 }
 
 // Two K/V stages (64 KB) per workgroup, two workgroups per CU: the next tile streams into LDS
 // while this one is computed, and the two workgroups overlap each other's MFMA and softmax work.
-template <int G>
-__global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) {
+template <int G, bool F16>
+__device__ __forceinline__ void attn_fwd_body(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) KvStageFwd ring[2];
 
   const int tid = threadIdx.x;
@@ -481,7 +493,7 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) {
     }
     RowIntervals iv;
     iv.at_tile(static_cast<int>((entry & ~kFullBit) * kTN), cb, ce, db, de);
-    fwd_tile(cur.k, cur.v, qf, oacc, m_run, l_run, !(entry & kFullBit), iv, a.scale_log2, offs, g);
+    fwd_tile<F16>(cur.k, cur.v, qf, oacc, m_run, l_run, !(entry & kFullBit), iv, a.scale_log2, offs, g);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's loads of tile t+1 have landed
     lds_barrier();
   };
@@ -494,16 +506,23 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) {
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   if (valid_q) {
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    store_row_c(a.out + qrow * a.ost + head * a.osh, oacc, inv, g);
+    store_row_c<F16>(a.out + qrow * a.ost + head * a.osh, oacc, inv, g);
     if (g == 0) a.lse[static_cast<int64_t>(head) * a.nq + qrow] =
         l_tot > 0.f ? (m_run + log2f(l_tot)) * kLn2 : kMaskValue;
   }
 }
 
+// bf16 and fp16 instances (one kernel name per element type).
+template <int G>
+__global__ void __launch_bounds__(kWave * G, 2) attn_fwd_kernel(AttnArgs a) { attn_fwd_body<G, false>(a); }
+template <int G>
+__global__ void __launch_bounds__(kWave * G, 2) attn_fwd_f16_kernel(AttnArgs a) { attn_fwd_body<G, true>(a); }
+
 // ---------------------------------------------------------------------------------------------
 // Backward prepare: delta = rowsum(dO * O) - dLSE, lse2 = LSE * log2(e) (16 lanes per row).
 // ---------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) attn_bwd_pre_kernel(AttnArgs a) {
+template <bool F16>
+__device__ __forceinline__ void attn_bwd_pre_body(AttnArgs a) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t row = t >> 4;  // row = head * nq + q
   const int chunk = static_cast<int>(t & 15);
@@ -515,7 +534,7 @@ __global__ void __launch_bounds__(256) attn_bwd_pre_kernel(AttnArgs a) {
     const uint4 o = load16(a.o + q * a.ost + head * a.osh + chunk * 8);
     const uint4 d = load16(a.dout + q * a.dost + head * a.dosh + chunk * 8);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += bf16_to_f32(half_of(o, e)) * bf16_to_f32(half_of(d, e));
+    for (int e = 0; e < 8; ++e) acc += elem_to_f32<F16>(half_of(o, e)) * elem_to_f32<F16>(half_of(d, e));
   }
 #pragma unroll
   for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
@@ -526,10 +545,14 @@ __global__ void __launch_bounds__(256) attn_bwd_pre_kernel(AttnArgs a) {
   }
 }
 
+__global__ void __launch_bounds__(256) attn_bwd_pre_kernel(AttnArgs a) { attn_bwd_pre_body<false>(a); }
+__global__ void __launch_bounds__(256) attn_bwd_pre_f16_kernel(AttnArgs a) { attn_bwd_pre_body<true>(a); }
+
 // Grid: (key tile, kv head) pairs. For key tiles split over several units, sums the units' fp32
 // partials in chunk order (deterministic) and writes bf16 dK (times the softmax scale) and dV; other
 // tiles were written directly by their unit.
-__global__ void __launch_bounds__(256) attn_bwd_acc_kernel(AttnArgs a) {
+template <bool F16>
+__device__ __forceinline__ void attn_bwd_acc_body(AttnArgs a) {
   const int hkv = blockIdx.x % a.hkv;
   const int64_t n = blockIdx.x / a.hkv;
   const int chunks = a.plan.b_chunks[n];
@@ -562,18 +585,22 @@ __global__ void __launch_bounds__(256) attn_bwd_acc_kernel(AttnArgs a) {
       }
     }
     u32x2 wk, wv;
-    wk.x = pack_bf16x2(k4[0] * a.scale, k4[1] * a.scale);
-    wk.y = pack_bf16x2(k4[2] * a.scale, k4[3] * a.scale);
-    wv.x = pack_bf16x2(v4[0], v4[1]);
-    wv.y = pack_bf16x2(v4[2], v4[3]);
+    wk.x = pack_elem2<F16>(k4[0] * a.scale, k4[1] * a.scale);
+    wk.y = pack_elem2<F16>(k4[2] * a.scale, k4[3] * a.scale);
+    wv.x = pack_elem2<F16>(v4[0], v4[1]);
+    wv.y = pack_elem2<F16>(v4[2], v4[3]);
     *reinterpret_cast<u32x2*>(a.dk + key * a.dkst + hkv * a.dksh + d) = wk;
     *reinterpret_cast<u32x2*>(a.dv + key * a.dvst + hkv * a.dvsh + d) = wv;
   }
 }
 
+__global__ void __launch_bounds__(256) attn_bwd_acc_kernel(AttnArgs a) { attn_bwd_acc_body<false>(a); }
+__global__ void __launch_bounds__(256) attn_bwd_acc_f16_kernel(AttnArgs a) { attn_bwd_acc_body<true>(a); }
+
 // ---------------------------------------------------------------------------------------------
 // dQ: query-major, same traversal and K/V ring as the forward. dQ^T = K^T dS^T.
 // ---------------------------------------------------------------------------------------------
+template <bool F16>
 __device__ __forceinline__ void dq_tile(const uint16_t* sk, const uint16_t* sv,
                                         const bf16x8 (&qf)[8], const bf16x8 (&df)[8],
                                         f32x16 (&dqacc)[4], float lse2, float delta, bool partial,
@@ -585,7 +612,7 @@ __device__ __forceinline__ void dq_tile(const uint16_t* sk, const uint16_t* sv,
   for (int kb = 0; kb < 2; ++kb) {
     bf16x8 dsb[2];
     f32x16 s, dp;
-    mfma_chains2<kDqAhead>(s, dp, RowOperand{sk + kb * 32 * kRowLd, ro},
+    mfma_chains2<kDqAhead, F16>(s, dp, RowOperand{sk + kb * 32 * kRowLd, ro},
                            RowOperand{sv + kb * 32 * kRowLd, ro}, qf, df);
     bf16x8 kcur[4];
     read_tr_first(kcur, sk + kb * 32 * kRowLd, tro);
@@ -598,14 +625,14 @@ __device__ __forceinline__ void dq_tile(const uint16_t* sk, const uint16_t* sv,
       const float p = fast_exp2(fmaf(s[r], scale_log2, neg_lse2));
       s[r] = p * (dp[r] - delta);
     }
-    dsb[0] = pack_c_half(s, 0);
-    dsb[1] = pack_c_half(s, 8);
-    mfma_tr_blocks<2>(dqacc, sk + kb * 32 * kRowLd, tro, kcur, dsb);
+    dsb[0] = pack_c_half<F16>(s, 0);
+    dsb[1] = pack_c_half<F16>(s, 8);
+    mfma_tr_blocks<2, F16>(dqacc, sk + kb * 32 * kRowLd, tro, kcur, dsb);
   }
 }
 
-template <int G>
-__global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
+template <int G, bool F16>
+__device__ __forceinline__ void attn_bwd_dq_body(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) KvStageFwd ring[2];
 
   const int tid = threadIdx.x;
@@ -665,13 +692,18 @@ __global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) {
     opaque(tro_t.hi);
     RowIntervals iv;
     iv.at_tile(static_cast<int>((entry & ~kFullBit) * kTN), cb, ce, db, de);
-    dq_tile(st.k, st.v, qf, df, dqacc, lse2, delta, !(entry & kFullBit), iv, a.scale_log2, ro_t,
+    dq_tile<F16>(st.k, st.v, qf, df, dqacc, lse2, delta, !(entry & kFullBit), iv, a.scale_log2, ro_t,
             tro_t, g);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // this wave's loads of tile t+1 have landed
     lds_barrier();
   }
-  if (valid_q) store_row_c(a.dq + qrow * a.dqst + head * a.dqsh, dqacc, a.scale, g);
+  if (valid_q) store_row_c<F16>(a.dq + qrow * a.dqst + head * a.dqsh, dqacc, a.scale, g);
 }
+
+template <int G>
+__global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_kernel(AttnArgs a) { attn_bwd_dq_body<G, false>(a); }
+template <int G>
+__global__ void __launch_bounds__(kWave * G, 2) attn_bwd_dq_f16_kernel(AttnArgs a) { attn_bwd_dq_body<G, true>(a); }
 
 // ---------------------------------------------------------------------------------------------
 // dK / dV: key-major. A workgroup owns one 128-key tile and walks one chunk of the (descending)
@@ -733,13 +765,13 @@ __device__ __forceinline__ void chain_first(uint4 (&x)[8], const Operand& ra) {
 
 // acc = A x B over the 128-dim reduction: A rows from LDS (`x` holds the first kDkdvAhead k-steps,
 // the rest are read kDkdvAhead steps ahead of their MFMA), B from registers.
-template <typename Operand>
+template <bool F16 = false, typename Operand>
 __device__ __forceinline__ f32x16 chain_rest(uint4 (&x)[8], const Operand& ra, const bf16x8 (&b)[8]) {
   f32x16 acc{};
 #pragma unroll
   for (int ds = 0; ds < 8; ++ds) {
     if (ds + kDkdvAhead < 8) x[ds + kDkdvAhead] = ra.step(ds + kDkdvAhead);
-    acc = mfma32(as_bf16x8(x[ds]), b[ds], acc);
+    acc = mfma32<F16>(as_bf16x8(x[ds]), b[ds], acc);
     ASPEC_STEP_FENCE();
   }
   return acc;
@@ -755,11 +787,12 @@ __device__ __forceinline__ void read_tr_32(bf16x8 (&f)[2][4], const uint16_t* ti
 }
 
 // acc[d] += F[ks][d] x B[ks] over a 32-row reduction, every operand in registers.
+template <bool F16 = false>
 __device__ __forceinline__ void mfma_regs_32(f32x16 (&acc)[4], const bf16x8 (&f)[2][4], const bf16x8 (&b)[2]) {
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-    for (int d = 0; d < 4; ++d) acc[d] = mfma32(f[ks][d], b[ks], acc[d]);
+    for (int d = 0; d < 4; ++d) acc[d] = mfma32<F16>(f[ks][d], b[ks], acc[d]);
 }
 
 // What each role carries over the barrier from one trip to the next: the operands of the products
@@ -781,6 +814,7 @@ struct DsCarry {  // dS wave: dP of its previous stage, that stage's Q^T fragmen
 // past `valid` hold copies of a real row and get an empty mask. `key_base` is the slice's first
 // key. A fully visible stage (a full tile with all rows real) skips the visibility words and the
 // mask.
+template <bool F16>
 __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf16x8 (&kf)[8],
                                             f32x16 (&dvacc)[4], PCarry& cy, bool live,
                                             float scale_log2, int w, int valid, bool all_visible,
@@ -796,7 +830,7 @@ __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf1
     for (int rq = 0; rq < 4; ++rq) l4[rq] = *reinterpret_cast<const f32x4*>(s.lse2 + rq * 8 + g * 4);
   }
   ASPEC_STEP_FENCE();
-  mfma_regs_32(dvacc, cy.d, cy.p);
+  mfma_regs_32<F16>(dvacc, cy.d, cy.p);
   ASPEC_STEP_FENCE();
   if (!live) return;
   if (!all_visible) {
@@ -807,7 +841,7 @@ __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf1
     }
     __builtin_amdgcn_wave_barrier();
   }
-  f32x16 sacc = chain_rest(x, RowOperandR{s.q, ro}, kf);  // rows: queries, lane: key
+  f32x16 sacc = chain_rest<F16>(x, RowOperandR{s.q, ro}, kf);  // rows: queries, lane: key
   read_tr_32(cy.d, s.dout, tro);
   ASPEC_STEP_FENCE();
   if (all_visible) {
@@ -828,8 +862,8 @@ __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf1
         sacc[rq * 4 + j] = __int_as_float(__float_as_int(p) & keep);
       }
   }
-  cy.p[0] = pack_c_half(sacc, 0);
-  cy.p[1] = pack_c_half(sacc, 8);
+  cy.p[0] = pack_c_half<F16>(sacc, 0);
+  cy.p[1] = pack_c_half<F16>(sacc, 8);
   px.p[w][0][lane] = __builtin_bit_cast(uint4, cy.p[0]);
   px.p[w][1][lane] = __builtin_bit_cast(uint4, cy.p[1]);
 }
@@ -838,6 +872,7 @@ __device__ __forceinline__ void dkdv_p_step(KvStage& s, PExchange& px, const bf1
 // delta and the Q^T fragments carried, P from the P wave's exchange buffer: the bf16 P the dV
 // product used; dS is rounded to bf16 for the dK product in any case); then, on a live stage:
 // dP = dO V^T (V slice in registers) and the stage's Q^T fragments and delta.
+template <bool F16>
 __device__ __forceinline__ void dkdv_ds_step(const KvStage& s, const PExchange& px,
                                              const bf16x8 (&vf)[8], f32x16 (&dkacc)[4],
                                              DsCarry& cy, bool live, int w, const RowOffsets& ro,
@@ -853,16 +888,22 @@ __device__ __forceinline__ void dkdv_ds_step(const KvStage& s, const PExchange& 
     const uint4& h = ph[rq >> 1];
     const uint32_t lo = (rq & 1) ? h.z : h.x;
     const uint32_t hi = (rq & 1) ? h.w : h.y;
-    const f32x4 p4 = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u),
-                      __uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
+    f32x4 p4;
+    if constexpr (F16) {
+      p4 = f32x4{elem_to_f32<true>(static_cast<uint16_t>(lo)), elem_to_f32<true>(static_cast<uint16_t>(lo >> 16)),
+                 elem_to_f32<true>(static_cast<uint16_t>(hi)), elem_to_f32<true>(static_cast<uint16_t>(hi >> 16))};
+    } else {
+      p4 = f32x4{__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u),
+                 __uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) dp[rq * 4 + j] = p4[j] * (dp[rq * 4 + j] - cy.delta[rq][j]);
   }
-  const bf16x8 dd[2] = {pack_c_half(dp, 0), pack_c_half(dp, 8)};
-  mfma_regs_32(dkacc, cy.q, dd);
+  const bf16x8 dd[2] = {pack_c_half<F16>(dp, 0), pack_c_half<F16>(dp, 8)};
+  mfma_regs_32<F16>(dkacc, cy.q, dd);
   ASPEC_STEP_FENCE();
   if (!live) return;
-  cy.dp = chain_rest(x, RowOperandR{s.dout, ro}, vf);
+  cy.dp = chain_rest<F16>(x, RowOperandR{s.dout, ro}, vf);
   read_tr_32(cy.q, s.q, tro);
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq) cy.delta[rq] = *reinterpret_cast<const f32x4*>(s.delta + rq * 8 + g * 4);
@@ -886,6 +927,7 @@ struct DkdvShared {
 // both the writes and the row reads bank-conflict free) so that every global write instruction
 // covers one contiguous key row: a bf16 store of the whole row (direct) or an fp32 store of the
 // unit's partial into its own slot (key tiles split over several units; no atomics).
+template <bool F16>
 __device__ __forceinline__ void dkdv_store(const f32x16 (&acc)[4], float* t, int64_t key_first,
                                            int64_t nk, bool direct, uint16_t* dst,
                                            int64_t dst_stride, float* ws, int64_t ws_stride,
@@ -908,14 +950,14 @@ __device__ __forceinline__ void dkdv_store(const f32x16 (&acc)[4], float* t, int
     const float* row = t + k * kHeadDim;
     const f32x2_t v = *reinterpret_cast<const f32x2_t*>(row + (((lane >> 1) ^ k) << 2) + (lane & 1) * 2);
     if (direct)
-      *reinterpret_cast<uint32_t*>(dst + key * dst_stride + 2 * lane) = pack_bf16x2(v[0] * mul, v[1] * mul);
+      *reinterpret_cast<uint32_t*>(dst + key * dst_stride + 2 * lane) = pack_elem2<F16>(v[0] * mul, v[1] * mul);
     else
       *reinterpret_cast<f32x2_t*>(ws + key * ws_stride + 2 * lane) = v;
   }
 }
 
-template <int G>
-__global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnArgs a) {
+template <int G, bool F16>
+__device__ __forceinline__ void attn_bwd_dkdv_body(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) DkdvShared sh;
   KvStage& st0 = sh.walk.st[0];
   KvStage& st1 = sh.walk.st[1];
@@ -1076,10 +1118,10 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
       int h, valid;
       row_base(i, q0, h, valid);
       const bool full = (tile_entry(i / G) & kFullBit) != 0;
-      dkdv_p_step(s_cur, x_cur, kvf, acc, pc, live, scale_log2, w, valid,
+      dkdv_p_step<F16>(s_cur, x_cur, kvf, acc, pc, live, scale_log2, w, valid,
                   full && valid == kBwdTileM, static_cast<int>(key0) + w * 32, ro, tro_t, lane);
     } else {
-      dkdv_ds_step(s_cur, x_prv, kvf, acc, dc, live, w, ro, tro_t, lane);
+      dkdv_ds_step<F16>(s_cur, x_prv, kvf, acc, dc, live, w, ro, tro_t, lane);
     }
     if (p_role && i + 3 < iters) issue(i + 3, s_nx);
     wait_loads(p_role ? (i + 2 < iters) + (i + 3 < iters) : (i + 2 < iters));
@@ -1111,13 +1153,18 @@ __global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnA
   const int64_t ws_slot = static_cast<int64_t>(chunk) * a.nk * ws_stride + hkv * kHeadDim;
   const int64_t key_first = key0 + w * 32;
   if (p_role)
-    dkdv_store(acc, sh.out[w], key_first, a.nk, direct, a.dv + hkv * a.dvsh, a.dvst,
+    dkdv_store<F16>(acc, sh.out[w], key_first, a.nk, direct, a.dv + hkv * a.dvsh, a.dvst,
                a.ws_dv + ws_slot, ws_stride, 1.f, lane);
   lds_barrier();
   if (!p_role)
-    dkdv_store(acc, sh.out[w], key_first, a.nk, direct, a.dk + hkv * a.dksh, a.dkst,
+    dkdv_store<F16>(acc, sh.out[w], key_first, a.nk, direct, a.dk + hkv * a.dksh, a.dkst,
                a.ws_dk + ws_slot, ws_stride, a.scale, lane);
 }
+
+template <int G>
+__global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_kernel(AttnArgs a) { attn_bwd_dkdv_body<G, false>(a); }
+template <int G>
+__global__ void __launch_bounds__(kWave * kDkdvWaves) attn_bwd_dkdv_f16_kernel(AttnArgs a) { attn_bwd_dkdv_body<G, true>(a); }
 
 int validate(const AttnArgs& a, int64_t head_dim) {
   if (head_dim != kHeadDim)
@@ -1143,6 +1190,16 @@ int validate(const AttnArgs& a, int64_t head_dim) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool stride_ok(int64_t s) { return s % 8 == 0; }
 
+// Element type of the attention entry points (the ASPEC_MASK_* codes of include/aspec_amd.h).
+constexpr int kDtypeBf16 = 4;
+constexpr int kDtypeF16 = 5;
+
+int check_dtype(int dtype) {
+  if (dtype != kDtypeBf16 && dtype != kDtypeF16)
+    return set_error(ASPEC_ERR_UNSUPPORTED, "DSpark attention computes in bf16 or fp16 (dtype code %d)", dtype);
+  return ASPEC_OK;
+}
+
 #define ASPEC_GROUP_DISPATCH(KERNEL, GROUP, GRID, STREAM, ARGS)                                  \
   switch (GROUP) {                                                                              \
     case 1: hipLaunchKernelGGL(KERNEL<1>, GRID, dim3(kWave * 1), 0, STREAM, ARGS); break;       \
@@ -1167,7 +1224,8 @@ extern "C" int aspec_dspark_attn_fwd(const void* q, int64_t q_stride_token, int6
                                      int64_t num_queries, int64_t num_keys, int64_t q_heads,
                                      int64_t kv_heads, int64_t head_dim, float scale, void* out,
                                      int64_t o_stride_token, int64_t o_stride_head, float* lse,
-                                     void* stream) {
+                                     int dtype, void* stream) {
+  if (int rc = check_dtype(dtype)) return rc;
   AttnArgs a = {};
   a.q = static_cast<const uint16_t*>(q); a.qst = q_stride_token; a.qsh = q_stride_head;
   a.k = static_cast<const uint16_t*>(k); a.kst = k_stride_token; a.ksh = k_stride_head;
@@ -1191,7 +1249,11 @@ extern "C" int aspec_dspark_attn_fwd(const void* q, int64_t q_stride_token, int6
   a.plan = plan_view(const_cast<void*>(plan), num_queries, num_keys);
   const dim3 grid(static_cast<uint32_t>(a.plan.nmf * a.hkv));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  ASPEC_GROUP_DISPATCH(attn_fwd_kernel, a.group, grid, s, a);
+  if (dtype == kDtypeF16) {
+    ASPEC_GROUP_DISPATCH(attn_fwd_f16_kernel, a.group, grid, s, a);
+  } else {
+    ASPEC_GROUP_DISPATCH(attn_fwd_kernel, a.group, grid, s, a);
+  }
   return check_launch("attn_fwd_kernel");
 }
 
@@ -1215,8 +1277,10 @@ extern "C" int aspec_dspark_attn_bwd_stages(
     int64_t num_keys, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float scale, void* dq,
     int64_t dq_stride_token, int64_t dq_stride_head, void* dk, int64_t dk_stride_token,
     int64_t dk_stride_head, void* dv, int64_t dv_stride_token, int64_t dv_stride_head,
-    void* workspace, void* stream) {
+    void* workspace, int dtype, void* stream) {
   if (stages <= 0 || stages > 15) return set_error(ASPEC_ERR_INVALID, "backward stage mask must be 1..15");
+  if (int rc = check_dtype(dtype)) return rc;
+  const bool f16 = dtype == kDtypeF16;
   AttnArgs a = {};
   a.q = static_cast<const uint16_t*>(q); a.qst = q_stride_token; a.qsh = q_stride_head;
   a.k = static_cast<const uint16_t*>(k); a.kst = k_stride_token; a.ksh = k_stride_head;
@@ -1255,31 +1319,49 @@ extern "C" int aspec_dspark_attn_bwd_stages(
 
   if (stages & 1) {
     const int64_t pre_threads = num_queries * q_heads * 16;
-    hipLaunchKernelGGL(attn_bwd_pre_kernel, dim3(static_cast<uint32_t>((pre_threads + 255) / 256)),
-                       dim3(256), 0, s, a);
+    const dim3 grid(static_cast<uint32_t>((pre_threads + 255) / 256));
+    if (f16)
+      hipLaunchKernelGGL(attn_bwd_pre_f16_kernel, grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(attn_bwd_pre_kernel, grid, dim3(256), 0, s, a);
     if ((rc = check_launch("attn_bwd_pre_kernel"))) return rc;
   }
   if (stages & 2) {
     const dim3 grid(static_cast<uint32_t>(a.plan.nmf * a.hkv));
-    ASPEC_GROUP_DISPATCH(attn_bwd_dq_kernel, a.group, grid, s, a);
+    if (f16) {
+      ASPEC_GROUP_DISPATCH(attn_bwd_dq_f16_kernel, a.group, grid, s, a);
+    } else {
+      ASPEC_GROUP_DISPATCH(attn_bwd_dq_kernel, a.group, grid, s, a);
+    }
     if ((rc = check_launch("attn_bwd_dq_kernel"))) return rc;
   }
   if (stages & 4) {
     const dim3 grid(static_cast<uint32_t>(a.plan.max_units * a.hkv)), block(kWave * kDkdvWaves);
-    switch (a.group) {  // the group size is a compile-time constant inside the walk
-      case 1: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<1>, grid, block, 0, s, a); break;
-      case 2: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<2>, grid, block, 0, s, a); break;
-      case 3: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<3>, grid, block, 0, s, a); break;
-      case 4: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<4>, grid, block, 0, s, a); break;
-      case 5: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<5>, grid, block, 0, s, a); break;
-      case 6: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<6>, grid, block, 0, s, a); break;
-      case 7: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<7>, grid, block, 0, s, a); break;
-      default: hipLaunchKernelGGL(attn_bwd_dkdv_kernel<8>, grid, block, 0, s, a); break;
+    // the group size is a compile-time constant inside the walk
+#define ASPEC_DKDV_DISPATCH(KERNEL)                                                   \
+  switch (a.group) {                                                                 \
+    case 1: hipLaunchKernelGGL(KERNEL<1>, grid, block, 0, s, a); break;              \
+    case 2: hipLaunchKernelGGL(KERNEL<2>, grid, block, 0, s, a); break;              \
+    case 3: hipLaunchKernelGGL(KERNEL<3>, grid, block, 0, s, a); break;              \
+    case 4: hipLaunchKernelGGL(KERNEL<4>, grid, block, 0, s, a); break;              \
+    case 5: hipLaunchKernelGGL(KERNEL<5>, grid, block, 0, s, a); break;              \
+    case 6: hipLaunchKernelGGL(KERNEL<6>, grid, block, 0, s, a); break;              \
+    case 7: hipLaunchKernelGGL(KERNEL<7>, grid, block, 0, s, a); break;              \
+    default: hipLaunchKernelGGL(KERNEL<8>, grid, block, 0, s, a); break;             \
+  }
+    if (f16) {
+      ASPEC_DKDV_DISPATCH(attn_bwd_dkdv_f16_kernel)
+    } else {
+      ASPEC_DKDV_DISPATCH(attn_bwd_dkdv_kernel)
     }
+#undef ASPEC_DKDV_DISPATCH
     if ((rc = check_launch("attn_bwd_dkdv_kernel"))) return rc;
   }
   if (stages & 8) {
-    hipLaunchKernelGGL(attn_bwd_acc_kernel, acc_grid, dim3(256), 0, s, a);
+    if (f16)
+      hipLaunchKernelGGL(attn_bwd_acc_f16_kernel, acc_grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(attn_bwd_acc_kernel, acc_grid, dim3(256), 0, s, a);
     rc = check_launch("attn_bwd_acc_kernel");
   }
   return rc;
@@ -1294,11 +1376,11 @@ extern "C" int aspec_dspark_attn_bwd(
     int64_t num_keys, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float scale, void* dq,
     int64_t dq_stride_token, int64_t dq_stride_head, void* dk, int64_t dk_stride_token,
     int64_t dk_stride_head, void* dv, int64_t dv_stride_token, int64_t dv_stride_head,
-    void* workspace, void* stream) {
+    void* workspace, int dtype, void* stream) {
   return aspec_dspark_attn_bwd_stages(
       15, q, q_stride_token, q_stride_head, k, k_stride_token, k_stride_head, v, v_stride_token,
       v_stride_head, out, o_stride_token, o_stride_head, dout, do_stride_token, do_stride_head,
       lse, dlse, endpoints, plan, num_queries, num_keys, q_heads, kv_heads, head_dim, scale, dq,
       dq_stride_token, dq_stride_head, dk, dk_stride_token, dk_stride_head, dv, dv_stride_token,
-      dv_stride_head, workspace, stream);
+      dv_stride_head, workspace, dtype, stream);
 }

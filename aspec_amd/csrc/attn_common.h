@@ -46,8 +46,38 @@ __device__ __forceinline__ int row_operand_off(int row, int g) {
   return row * kRowLd + ((g ^ swz(row)) << 3);
 }
 
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+
+// Operands are carried as 16-byte bf16x8 values whatever the element type; F16 selects the fp16
+// instruction (v_mfma_f32_32x32x16_f16) over the same bits.
+template <bool F16 = false>
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b),
+                                                  c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Two floats -> a packed pair of the element type, round-to-nearest-even.
+template <bool F16 = false>
+__device__ __forceinline__ uint32_t pack_elem2(float lo, float hi) {
+  if constexpr (F16) {
+    const f32x2_t x = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, f16x2_t));
+  } else {
+    return pack_bf16x2(lo, hi);
+  }
+}
+
+// One element of the element type (bits) -> float.
+template <bool F16 = false>
+__device__ __forceinline__ float elem_to_f32(uint16_t v) {
+  if constexpr (F16)
+    return static_cast<float>(__builtin_bit_cast(_Float16, v));
+  else
+    return bf16_to_f32(v);
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) {
@@ -66,12 +96,13 @@ __device__ __forceinline__ uint16_t half_of(const uint4& v, int e) {
 
 // Packs C registers [base, base+8) into the bf16 operand whose slot e pairs with C row
 // (e/4)*8 + g*4 + e%4 of the 16-row half starting at base/8*16.
+template <bool F16 = false>
 __device__ __forceinline__ bf16x8 pack_c_half(const f32x16& c, int base) {
   uint4 v;
-  v.x = pack_bf16x2(c[base + 0], c[base + 1]);
-  v.y = pack_bf16x2(c[base + 2], c[base + 3]);
-  v.z = pack_bf16x2(c[base + 4], c[base + 5]);
-  v.w = pack_bf16x2(c[base + 6], c[base + 7]);
+  v.x = pack_elem2<F16>(c[base + 0], c[base + 1]);
+  v.y = pack_elem2<F16>(c[base + 2], c[base + 3]);
+  v.z = pack_elem2<F16>(c[base + 4], c[base + 5]);
+  v.w = pack_elem2<F16>(c[base + 6], c[base + 7]);
   return as_bf16x8(v);
 }
 

@@ -26,6 +26,6 @@ int check_launch(const char* what) {
 
 }  // namespace aspec
 
-extern "C" int aspec_abi_version(void) { return 14; }
+extern "C" int aspec_abi_version(void) { return 15; }
 
 extern "C" const char* aspec_last_error(void) { return aspec::g_last_error; }

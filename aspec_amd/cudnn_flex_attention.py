@@ -15,8 +15,8 @@ work unchanged.
 - GQA: the kernels reduce the query heads of each KV group inside the workgroup (joint GQA), so
   every `gqa_mode` and `physical_gqa` runs the same kernels; the reference's query-head folding is
   a cuDNN layout choice with no counterpart here and does not change the result.
-- Computed in bf16 (fp32 accumulation) with head_dim 128. fp16 inputs and the materialised-MLA
-  (Dqk, Dv) = (192, 128) shape raise NotImplementedError. Rows without a visible key return O = 0
+- Computed in bf16 or fp16 (fp32 accumulation) with head_dim 128. The materialised-MLA
+  (Dqk, Dv) = (192, 128) shape raises NotImplementedError. Rows without a visible key return O = 0
   and LSE = -1e30, the convention of the Direct-CP path (direct_cp.py:470-477).
 """
 
@@ -275,8 +275,6 @@ def cudnn_flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Te
     resolve_cudnn_gqa_mode(gqa_mode, physical_gqa=physical_gqa)
     if dims != (128, 128):
         raise NotImplementedError("materialized MLA (Dqk=192) is outside the DSpark GQA kernels of this build")
-    if query.dtype != torch.bfloat16:
-        raise NotImplementedError("the DSpark kernels compute in bf16 (fp32 accumulation); got FP16")
     plan = mask.plan_for(query, key, value, pack_gqa=pack_gqa)
     if query.ndim == 4:
         batch, lq = query.shape[:2]

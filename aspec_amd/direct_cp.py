@@ -294,7 +294,7 @@ class _DSparkAttention(torch.autograd.Function):
                 _lib.ptr(q), q.stride(2), q.stride(1), _lib.ptr(k), k.stride(2), k.stride(1),
                 _lib.ptr(v), v.stride(2), v.stride(1), _lib.ptr(endpoints), _lib.ptr(plan),
                 nq, nk, hq, hkv, d, float(scale), _lib.ptr(out), out.stride(1), out.stride(2),
-                _lib.ptr(lse), _lib.stream_handle(q.device),
+                _lib.ptr(lse), _lib.mask_dtype_code(q), _lib.stream_handle(q.device),
             )
         ctx.save_for_backward(q, k, v, out, lse, endpoints, plan)
         ctx.scale = float(scale)
@@ -325,7 +325,7 @@ class _DSparkAttention(torch.autograd.Function):
             _lib.ptr(dout), dout.stride(2), dout.stride(1), _lib.ptr(lse), _lib.ptr(dlse_c),
             _lib.ptr(endpoints), _lib.ptr(plan), nq, nk, hq, hkv, d, ctx.scale,
             _lib.ptr(dq), dq.stride(1), dq.stride(2), _lib.ptr(dk), dk.stride(1), dk.stride(2),
-            _lib.ptr(dv), dv.stride(1), dv.stride(2), _lib.ptr(workspace),
+            _lib.ptr(dv), dv.stride(1), dv.stride(2), _lib.ptr(workspace), _lib.mask_dtype_code(q),
             _lib.stream_handle(q.device),
         )
         # dQ and dK/dV depend only on the prepare stage: dQ runs on a second stream (default
@@ -384,13 +384,21 @@ def _join_batch(x: Tensor) -> Tensor:
     return x.transpose(1, 2).reshape(1, b * n, h, d).transpose(1, 2)
 
 
+def _check_dtypes(query: Tensor, key: Tensor, value: Tensor) -> None:
+    """bf16 or fp16 Q/K/V of one dtype (the reference's GPU paths take both: FA4 for either,
+    direct_cp.py:1063-1068; cuDNN, cudnn_flex_attention.py:353-356); fp32 accumulation."""
+    if query.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError("aspec_amd DSpark attention computes in bf16 or fp16 (fp32 accumulation)")
+    if key.dtype != query.dtype or value.dtype != query.dtype:
+        raise TypeError("Q/K/V must have the same dtype")
+
+
 def dspark_attention(query: Tensor, key: Tensor, value: Tensor, metadata: DirectCPMetadata,
                      scale: float) -> tuple[Tensor, Tensor]:
     """HIP block-sparse DSpark attention over the metadata's rows: (out [B,Hq,Nq,D], lse [B,Hq,Nq])."""
     if not query.is_cuda:
         raise ValueError("aspec_amd attention runs on the GPU; got a CPU tensor")
-    if query.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
-        raise NotImplementedError("aspec_amd DSpark attention computes in bf16 (fp32 accumulation)")
+    _check_dtypes(query, key, value)
     batch = query.shape[0]
     if batch != metadata.anchor_positions.shape[0]:
         raise ValueError("query batch must match the metadata batch")
@@ -495,8 +503,7 @@ def direct_cp_partial_attention(query_full: Tensor, key: Tensor, value: Tensor,
         raise ValueError(f"expected {metadata.num_blocks * metadata.block_size} gathered queries")
     if not query_full.is_cuda:
         raise ValueError("aspec_amd attention runs on the GPU; got a CPU tensor")
-    if query_full.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
-        raise NotImplementedError("aspec_amd DSpark attention computes in bf16 (fp32 accumulation)")
+    _check_dtypes(query_full, key, value)
     if query_full.shape[1] % key.shape[1]:
         raise ValueError("query heads must be divisible by the matching KV head count")
     if metadata.backend == "math":

@@ -183,7 +183,8 @@ int aspec_dspark_plan_build(const int32_t* endpoints, int64_t num_queries, int64
                             void* plan, void* stream);
 
 /*
- * DSpark block-sparse attention forward (bf16 in, fp32 accumulation, bf16 out, fp32 natural-log LSE).
+ * DSpark block-sparse attention forward (bf16 or fp16 in, fp32 accumulation, out in the input type,
+ * fp32 natural-log LSE).
  *
  * Replaces the forward of `direct_cp_attention_from_kv` (aspec/models/ops/direct_cp.py:1047-1100)
  * at CP=1 via `thd_fa4_attention` (thd_attention.py:136-220) / `_cudnn_partial`
@@ -191,7 +192,9 @@ int aspec_dspark_plan_build(const int32_t* endpoints, int64_t num_queries, int64
  * visible key get O = 0 and LSE = -1e30.
  * q: [Nq] x [Hq] x [D] with element strides (q_stride_token, q_stride_head), unit stride on D;
  * k, v: [K] x [Hkv] x [D] likewise; out: [Nq] x [Hq] x [D]; lse: [Hq][Nq] contiguous.
- * Requires D == 128, Hq % Hkv == 0, Hq/Hkv <= 8, 16-byte aligned rows.
+ * Requires D == 128, Hq % Hkv == 0, Hq/Hkv <= 8, 16-byte aligned rows. dtype is ASPEC_MASK_BF16
+ * or ASPEC_MASK_F16 (Q, K, V, out and the P.V operand; `cudnn_flex_attention` accepts both,
+ * aspec/models/ops/cudnn_flex_attention.py:353-356); anything else returns ASPEC_ERR_UNSUPPORTED.
  */
 int aspec_dspark_attn_fwd(const void* q, int64_t q_stride_token, int64_t q_stride_head,
                           const void* k, int64_t k_stride_token, int64_t k_stride_head,
@@ -199,7 +202,7 @@ int aspec_dspark_attn_fwd(const void* q, int64_t q_stride_token, int64_t q_strid
                           const int32_t* endpoints, const void* plan, int64_t num_queries,
                           int64_t num_keys, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                           float scale, void* out, int64_t o_stride_token, int64_t o_stride_head,
-                          float* lse, void* stream);
+                          float* lse, int dtype, void* stream);
 
 /*
  * Workspace (bytes) needed by aspec_dspark_attn_bwd: per-row delta and log2-scaled LSE
@@ -211,8 +214,9 @@ int aspec_dspark_attn_bwd_workspace_bytes(int64_t num_queries, int64_t num_keys,
                                           int64_t kv_heads, size_t* bytes);
 
 /*
- * DSpark attention backward: dQ, dK, dV (bf16) from dO (bf16) and an optional dLSE (fp32 [Hq][Nq],
- * NULL = zero). Replaces FA4's block-sparse backward and `_InternalGQA.backward`
+ * DSpark attention backward: dQ, dK, dV from dO (all in the dtype of the forward: ASPEC_MASK_BF16
+ * or ASPEC_MASK_F16) and an optional dLSE (fp32 [Hq][Nq], NULL = zero). Replaces FA4's
+ * block-sparse backward and `_InternalGQA.backward`
  * (aspec/models/ops/cudnn_gqa_backward.py:128-342): the q heads of one KV group are reduced
  * inside the kernel. Every output is deterministic (bitwise equal across runs): dQ is written once
  * per row; a key tile whose query list fits one work unit writes its dK/dV rows once; a key tile
@@ -231,14 +235,14 @@ int aspec_dspark_attn_bwd(const void* q, int64_t q_stride_token, int64_t q_strid
                           int64_t dq_stride_token, int64_t dq_stride_head, void* dk,
                           int64_t dk_stride_token, int64_t dk_stride_head, void* dv,
                           int64_t dv_stride_token, int64_t dv_stride_head, void* workspace,
-                          void* stream);
+                          int dtype, void* stream);
 
 /*
  * The same backward, one stage at a time: `stages` is a bit mask of 1 = prepare
  * (delta = rowsum(dO*O) - dLSE and LSE*log2(e) into the workspace; the role of the reference's
  * preprocess launch, aspec/kernels/cutedsl/cudnn_gqa/preprocess.py:44-333), 2 = dQ, 4 = dK/dV (the
  * main launch, cudnn_gqa_backward.py:276-296), 8 = finalize (split-tile partials summed in unit
- * order to bf16, the role of postprocess.py:38-581). Stages run in that order; a later stage needs the workspace an earlier
+ * order to the element type, the role of postprocess.py:38-581). Stages run in that order; a later stage needs the workspace an earlier
  * call prepared on the same stream.
  */
 int aspec_dspark_attn_bwd_stages(int stages, const void* q, int64_t q_stride_token,
@@ -252,7 +256,7 @@ int aspec_dspark_attn_bwd_stages(int stages, const void* q, int64_t q_stride_tok
                                  int64_t head_dim, float scale, void* dq, int64_t dq_stride_token,
                                  int64_t dq_stride_head, void* dk, int64_t dk_stride_token,
                                  int64_t dk_stride_head, void* dv, int64_t dv_stride_token,
-                                 int64_t dv_stride_head, void* workspace, void* stream);
+                                 int64_t dv_stride_head, void* workspace, int dtype, void* stream);
 
 /* Floats of per-row statistics written by aspec_ce_l1_fwd and read by aspec_ce_l1_bwd (8). */
 int aspec_loss_stats_floats(void);

@@ -2,7 +2,10 @@
 
 Tolerances (bf16 inputs, fp32 accumulation) follow the reference's own bf16-GPU-vs-math bars
 (tests/test_thd_attention.py:218-225): atol = rtol = 0.025 for O and LSE, 0.04 for dQ/dK/dV.
-Max-abs and relative-L2 errors are printed for every case.
+fp16 inputs (which the reference's cuDNN and FA4 routes also accept) are held to the same bars,
+and additionally to a relative-L2 error 4x below the bf16 run's on the same inputs, so a path
+that silently computed in bf16 would fail. Max-abs and relative-L2 errors are printed for every
+case.
 """
 
 import numpy as np
@@ -17,13 +20,13 @@ from oracle import metadata as M
 pytestmark = pytest.mark.gpu
 
 
-def _inputs(w, device, seed, scale_in=0.5, token_major=True):
+def _inputs(w, device, seed, scale_in=0.5, token_major=True, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
     hq, hkv, d = w.q_heads, w.kv_heads, w.head_dim
-    q = (torch.randn(w.num_queries, hq, d, generator=g) * scale_in).bfloat16()
-    k = (torch.randn(w.num_keys, hkv, d, generator=g) * scale_in).bfloat16()
-    v = (torch.randn(w.num_keys, hkv, d, generator=g) * scale_in).bfloat16()
-    dout = torch.randn(w.num_queries, hq, d, generator=g).bfloat16()
+    q = (torch.randn(w.num_queries, hq, d, generator=g) * scale_in).to(dtype)
+    k = (torch.randn(w.num_keys, hkv, d, generator=g) * scale_in).to(dtype)
+    v = (torch.randn(w.num_keys, hkv, d, generator=g) * scale_in).to(dtype)
+    dout = torch.randn(w.num_queries, hq, d, generator=g).to(dtype)
     dlse = torch.randn(hq, w.num_queries, generator=g) * 0.1
     def dev(x):
         x = x.to(device)[None].transpose(1, 2)  # [1, H, L, D] view of token-major storage
@@ -39,9 +42,9 @@ def _report(name, got, ref):
     return err, rel
 
 
-def _check(w, device, seed=0, masks=None, token_major=True, use_dlse=True):
+def _check(w, device, seed=0, masks=None, token_major=True, use_dlse=True, dtype=torch.bfloat16):
     masks = masks or {}
-    (q, k, v), dout, dlse = _inputs(w, device, seed, token_major=token_major)
+    (q, k, v), dout, dlse = _inputs(w, device, seed, token_major=token_major, dtype=dtype)
     meta = W.metadata_for(w, device, **masks)
     scale = w.head_dim ** -0.5
     out, lse = direct_cp_attention_from_kv(q, k, v, meta, scale)
@@ -59,16 +62,17 @@ def _check(w, device, seed=0, masks=None, token_major=True, use_dlse=True):
         cpu(q), cpu(k), cpu(v), vis, scale, dout=cpu(dout),
         dlse=cpu(dlse) if use_dlse else None, dtype=torch.float32)
     keep = torch.as_tensor(vis.any(-1))
-    _report("O", cpu(out), r_out)
+    assert out.dtype == dtype and q.grad.dtype == dtype and k.grad.dtype == dtype
+    rels = {"O": _report("O", cpu(out), r_out)[1]}
     torch.testing.assert_close(cpu(out), r_out, atol=0.025, rtol=0.025)
     assert torch.all(cpu(lse)[:, ~keep] == A.MASK_VALUE)
     assert torch.all(cpu(out)[:, ~keep] == 0)
     _report("LSE", cpu(lse)[:, keep], r_lse[:, keep])
     torch.testing.assert_close(cpu(lse)[:, keep], r_lse[:, keep], atol=0.025, rtol=0.025)
     for name, got, ref in (("dQ", q.grad, r_dq), ("dK", k.grad, r_dk), ("dV", v.grad, r_dv)):
-        _report(name, cpu(got), ref)
+        rels[name] = _report(name, cpu(got), ref)[1]
         torch.testing.assert_close(cpu(got), ref, atol=0.04, rtol=0.04)
-    return meta
+    return meta, rels
 
 
 def test_reference_large_gpu_layout(gpu):
@@ -80,7 +84,7 @@ def test_reference_large_gpu_layout(gpu):
     keep = np.ones(80, bool)
     keep[13] = False
     w = W.from_layout("ref_large", lengths, anchors, docs[anchors], 7, keep=keep, q_heads=4, kv_heads=2)
-    meta = _check(w, gpu, seed=79)
+    meta, _ = _check(w, gpu, seed=79)
     assert meta.attention_observation["backward_observed"]
     assert meta.attention_observation["qkv_format"] == "thd"
 
@@ -109,6 +113,19 @@ def test_config1_fwd_bwd(gpu, seed):
 
 def test_config1_head_major_inputs_without_dlse(gpu):
     _check(W.config1(1), gpu, seed=1, token_major=False, use_dlse=False)
+
+
+@pytest.mark.parametrize("group", [1, 4, 5, 8])
+def test_fp16_inputs(gpu, group):
+    """fp16 Q/K/V (fp16 MFMA, P and dS rounded to fp16, fp16 outputs) against the same oracle:
+    within the bars, and at least 4x below the bf16 path's relative-L2 error on the same inputs
+    (fp16 keeps 3 more mantissa bits)."""
+    w = W.config1(4)
+    w.q_heads, w.kv_heads = 2 * group, 2
+    _, r16 = _check(w, gpu, seed=20 + group, dtype=torch.float16)
+    _, rbf = _check(w, gpu, seed=20 + group, dtype=torch.bfloat16)
+    for name in r16:
+        assert r16[name] * 4 < rbf[name], (name, r16[name], rbf[name])
 
 
 @pytest.mark.parametrize("group", [1, 2, 3, 5, 6, 7, 8])

@@ -165,10 +165,12 @@ def _padded_config1_batch(seeds=(0, 1), T=4096):
     return anchors, keep, docs
 
 
-def test_cudnn_flex_attention_dflash_call_padded_bshd_batch(gpu):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_cudnn_flex_attention_dflash_call_padded_bshd_batch(gpu, dtype):
     """The Draft layer's own call (dflash.py:932-942): BSHD Q/K/V, mask from build_dspark_mla_mask
     with packed documents, pack_gqa=False, physical_gqa=True; forward, LSE and all gradients of a
-    2-row padded batch against the fp32 oracle under the mask_mod's dense visibility."""
+    2-row padded batch against the fp32 oracle under the mask_mod's dense visibility, in bf16 and
+    in fp16 (the reference's cuDNN route takes both, cudnn_flex_attention.py:353-356)."""
     anchors, keep, docs = _padded_config1_batch()
     T, block = docs.shape[1], 16
     mask = _mask_gpu(gpu, anchors, keep, T, block, docs)
@@ -176,17 +178,17 @@ def test_cudnn_flex_attention_dflash_call_padded_bshd_batch(gpu):
                                   F.dspark_mla_mask(anchors, keep, T, block, ctx_doc_ids=docs))
     bsz, lq, nk = anchors.shape[0], anchors.shape[1] * block, T + anchors.shape[1] * block
     g = torch.Generator().manual_seed(17)
-    q = (torch.randn(bsz, lq, 32, 128, generator=g) * 0.5).bfloat16()
-    k = (torch.randn(bsz, nk, 8, 128, generator=g) * 0.5).bfloat16()
-    v = (torch.randn(bsz, nk, 8, 128, generator=g) * 0.5).bfloat16()
-    dout = torch.randn(bsz, lq, 32, 128, generator=g).bfloat16()
+    q = (torch.randn(bsz, lq, 32, 128, generator=g) * 0.5).to(dtype)
+    k = (torch.randn(bsz, nk, 8, 128, generator=g) * 0.5).to(dtype)
+    v = (torch.randn(bsz, nk, 8, 128, generator=g) * 0.5).to(dtype)
+    dout = torch.randn(bsz, lq, 32, 128, generator=g).to(dtype)
     dlse = torch.randn(bsz, 32, lq, generator=g) * 0.1
     results = {}
     for mode in ("auto", "internal"):
         qd, kd, vd = (t.to(gpu).requires_grad_() for t in (q, k, v))
         out, lse = cudnn_flex_attention(qd, kd, vd, mask=mask, scale=128 ** -0.5, pack_gqa=False,
                                         physical_gqa=True, gqa_mode=mode, return_lse=True)
-        assert out.shape == (bsz, lq, 32, 128) and lse.shape == (bsz, 32, lq)
+        assert out.shape == (bsz, lq, 32, 128) and lse.shape == (bsz, 32, lq) and out.dtype == dtype
         ((out.float() * dout.to(gpu).float()).sum() + (lse * dlse.to(gpu)).sum()).backward()
         torch.cuda.synchronize()
         results[mode] = [x.detach().cpu() for x in (out, lse, qd.grad, kd.grad, vd.grad)]
@@ -246,8 +248,8 @@ def test_cudnn_flex_attention_rejects_what_the_reference_rejects(gpu):
         cudnn_flex_attention(q[..., :64], k[..., :64], k[..., :64], mask=mask, scale=1.0)
     with pytest.raises(ValueError, match="GQA mode"):
         cudnn_flex_attention(q, k, k, mask=mask, scale=1.0, gqa_mode="bogus")
-    with pytest.raises(NotImplementedError, match="bf16"):
-        cudnn_flex_attention(q.half(), k.half(), k.half(), mask=mask, scale=1.0)
+    with pytest.raises(TypeError, match="same dtype"):
+        cudnn_flex_attention(q, k.half(), k.half(), mask=mask, scale=1.0)
 
 
 def _direct_cp_oracle(anchors, keep, positions, docs, adocs, block, seq, q, k, v, dout, dlse, b):

@@ -42,10 +42,13 @@ def test_size_queries_and_error_codes_without_gpu():
         _lib.check(lib.aspec_thd_tile_metadata(None, 0, 10, 256, 128, 1, *([None] * 10)))
     with pytest.raises(NotImplementedError, match="head_dim 128"):
         _lib.check(lib.aspec_dspark_attn_fwd(None, 0, 0, None, 0, 0, None, 0, 0, None, None,
-                                             16, 48, 4, 2, 64, 0.1, None, 0, 0, None, None))
+                                             16, 48, 4, 2, 64, 0.1, None, 0, 0, None, 4, None))
     with pytest.raises(ValueError, match="divisible"):
         _lib.check(lib.aspec_dspark_attn_fwd(None, 0, 0, None, 0, 0, None, 0, 0, None, None,
-                                             16, 48, 5, 2, 128, 0.1, None, 0, 0, None, None))
+                                             16, 48, 5, 2, 128, 0.1, None, 0, 0, None, 4, None))
+    with pytest.raises(NotImplementedError, match="bf16 or fp16"):
+        _lib.check(lib.aspec_dspark_attn_fwd(None, 0, 0, None, 0, 0, None, 0, 0, None, None,
+                                             16, 48, 4, 2, 128, 0.1, None, 0, 0, None, 0, None))
     # the segmented AdamW validates its host table before any launch
     assert lib.aspec_adamw_state_bytes() == 40 + 16 * 64  # step, coef, skip, norm + per-segment counts
 
