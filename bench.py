@@ -30,12 +30,12 @@ After the main measurement attention forward + backward alone is timed under "at
 config 1 also with the CPU math path's milliseconds) and on the reference's own published workload
 (B = 7, 10 x 4096 + 40960 + 49152 context tokens, 6144 anchors; tests/golden/dspark_b7_workload.json)
 beside the reference's SM100 figures. Those timings follow the reference's kernel-benchmark
-contract (tools/performance/bench_dspark_b7_attention.py:196-243; docs/dspark_attn_kernel_optimization.md:159):
-forward, backward and both, each captured once in a HIP graph; a 256 MiB cache flush before each
-window of 10 graph replays, 11 windows, the first 2 discarded, median of 9. The same F+B launched
-from the host is reported beside it. The full one-layer DSpark training step of BASELINE config 5 (forward, loss,
-backward and the fused AdamW) is timed on its own and reported under "config5_layer_step" (skip
-with --no-layer-step).
+contract (tools/performance/bench_dspark_b7_attention.py:196-243;
+docs/dspark_attn_kernel_optimization.md:159): forward, backward and both, each captured once in a
+HIP graph; a 256 MiB cache flush before each window of 10 graph replays, 11 windows, the first 2
+discarded, median of 9. The same F+B launched from the host is reported beside it. The full
+one-layer DSpark training step of BASELINE config 5 (forward, loss, backward and the fused AdamW)
+is timed on its own and reported under "config5_layer_step" (skip with --no-layer-step).
 After the timed work, "parity" compares the HIP outputs with the oracle on the bench's own
 config-2 inputs (every element of the attention outputs; 512 sampled loss rows), with max-abs and
 relative-L2 errors and the reference's tolerances (skip with --no-parity).
