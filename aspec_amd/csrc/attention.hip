@@ -607,9 +607,12 @@ __device__ __forceinline__ void dq_tile(const uint16_t* sk, const uint16_t* sv,
                                         const RowIntervals& iv, float scale_log2, int ro,
                                         const TrOffsets& tro, int g) {
   const float neg_lse2 = -lse2;
-  // One 32-key half at a time: dS of the half goes straight into dQ (8 registers of dS live).
+  // One 32-key half at a time: dS of the half goes straight into dQ (8 registers of dS live). A
+  // half that no row of the tile sees (a draft tile's other block pair, keys across a document
+  // boundary) is skipped: its P, and so its dS and its dQ terms, are exact zeros.
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
+    if (partial && __ballot(iv.word(kb, g) != 0u) == 0ull) continue;
     bf16x8 dsb[2];
     f32x16 s, dp;
     mfma_chains2<kDqAhead, F16>(s, dp, RowOperand{sk + kb * 32 * kRowLd, ro},
