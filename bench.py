@@ -389,6 +389,10 @@ def attention_timing(w, device, reps, flush):
     times = {p: contract_ms(g.replay, flush) for p, (g, _) in graphs.items()}
     del graphs
     torch.cuda.synchronize()
+    # The eager pass below runs on the default stream: drop the capture stream's autograd graph
+    # and give Q/K/V fresh leaves, so no gradient-accumulator node of that stream stays alive.
+    run.prepared = None
+    run.q, run.k, run.v = (x.detach().requires_grad_() for x in (run.q, run.k, run.v))
     overlap = backward_overlap()
     set_backward_overlap(False)
     _timing.reset()
