@@ -279,13 +279,8 @@ __device__ __forceinline__ void store_row_c(uint16_t* dst, const f32x16 (&acc)[4
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
 }
-__device__ __forceinline__ void lds_load16(const void* src, void* lds_wave_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :
-               : "s"(lds_address(lds_wave_base)), "v"(src)
-               : "memory", "m0");
-}
-// Same, addressed as a wave-uniform 64-bit base (SGPRs) plus a 32-bit per-lane byte offset.
+// 16 bytes per lane, addressed as a wave-uniform 64-bit base (SGPRs) plus a 32-bit per-lane byte
+// offset.
 __device__ __forceinline__ void lds_load16_at(const void* base, uint32_t byte_off, void* lds_wave_base) {
   // readfirstlane returns int: go through uint32_t so the low word is zero-extended, not
   // sign-extended into the high word.
@@ -298,6 +293,7 @@ __device__ __forceinline__ void lds_load16_at(const void* base, uint32_t byte_of
                : "s"(lds_address(lds_wave_base)), "v"(byte_off), "s"(sbase)
                : "memory", "m0");
 }
+// Same with 4 bytes per lane.
 __device__ __forceinline__ void lds_load4_at(const void* base, uint32_t byte_off, void* lds_wave_base) {
   const uint64_t b = reinterpret_cast<uintptr_t>(base);
   const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
@@ -306,12 +302,6 @@ __device__ __forceinline__ void lds_load4_at(const void* base, uint32_t byte_off
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
                :
                : "s"(lds_address(lds_wave_base)), "v"(byte_off), "s"(sbase)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void lds_load4(const void* src, void* lds_wave_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
-               :
-               : "s"(lds_address(lds_wave_base)), "v"(src)
                : "memory", "m0");
 }
 
